@@ -1,0 +1,123 @@
+"""ctypes binding of libattnlab.so, the C ABI declared in include/attnlab.h.
+
+torch is imported before the library is opened: torch ships its own HIP runtime under the soname libamdhip64.so.7,
+and the dynamic loader then resolves the library's libamdhip64.so.7 dependency to that same runtime, so the kernels
+launch on torch's streams and see torch's allocations. There is no fallback path: when the library is missing or
+cannot load, every op raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libattnlab.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2
+ORDER_POSITION, ORDER_SCORE = 0, 1
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+
+_p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/attnlab.h one to one
+SIGNATURES = {
+    "attnlab_abi_version": (_i, []),
+    "attnlab_last_error": (ctypes.c_char_p, []),
+    "attnlab_target": (ctypes.c_char_p, []),
+    "attnlab_score_grouped": (_i, [_p] * 8 + [_i64] + [_i] * 10 + [_p]),
+    "attnlab_score_prologue": (_i, [_p] * 6 + [_i] * 7 + [_p]),
+    "attnlab_project_keys": (_i, [_p, _i64, _i64, _p, _p] + [_i] * 7 + [_p]),
+    "attnlab_score_lightning": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 8 + [_p]),
+    "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
+    "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p]),
+    "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
+    "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
+    "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
+    "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _i64, _p, _p, _p, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+_load_error: str | None = None
+
+
+def _open():
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            _load_error = f"{LIB_PATH} is not built (run __graft_entry__.build())"
+            raise RuntimeError(_load_error)
+        try:
+            lib = ctypes.CDLL(LIB_PATH)
+        except OSError as e:  # pragma: no cover - depends on the host
+            _load_error = f"cannot load {LIB_PATH}: {e}"
+            raise RuntimeError(_load_error) from e
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        if lib.attnlab_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {lib.attnlab_abi_version()}, this binding expects {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def lib():
+    """The loaded library; raises RuntimeError when it is not built or cannot load."""
+    return _lib if _lib is not None else _open()
+
+
+def loadable() -> bool:
+    try:
+        lib()
+        return True
+    except RuntimeError:
+        return False
+
+
+def gpu_available() -> bool:
+    """A HIP device is visible and the library loads (the counterpart of metal_*.available())."""
+    return torch.cuda.is_available() and loadable()
+
+
+def call(name: str, *args) -> None:
+    """Invoke a C-ABI entry point and turn a non-zero status into ValueError / RuntimeError."""
+    rc = getattr(lib(), name)(*args)
+    if rc != ATTNLAB_OK:
+        msg = (lib().attnlab_last_error() or b"").decode(errors="replace")
+        if rc == ATTNLAB_EINVAL:
+            raise ValueError(f"{name}: {msg}")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def stream_of(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device` (kernels launch where torch would launch)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class Workspace:
+    """Growable device scratch owned by one op object (split-K partials, intermediate scores and row lists).
+
+    Two launches that share one Workspace must be ordered on one stream. Grow it (one eager call) before capturing
+    the launches in a HIP graph, so no allocation happens under capture.
+    """
+
+    def __init__(self):
+        self._bytes: dict = {}
+
+    def bytes(self, device: torch.device, nbytes: int, tag: str = "main") -> torch.Tensor:
+        key = (device, tag)
+        buf = self._bytes.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            self._bytes[key] = buf
+        return buf

@@ -1,0 +1,203 @@
+"""Gather-free decode attention on gfx950: the HIP replacement of the reference's Metal P1 kernels.
+
+`HipAttend.__call__` keeps the signature, shapes, dtypes and ValueError contract of `MetalAttend.__call__`
+(src/attention_lab/metal_attend.py:177-250), including the interleaved [G, C, 2, d] diagnostic layout, and
+`model_views` is the same batch-1 adapter (metal_attend.py:253-259). Limits are wider than the Metal kernel's:
+h <= 8 query heads per group (Metal: 4). Listed positions outside [0, C) are skipped by the kernel, never read.
+
+Beyond the reference: `attend` (batched [B,G,...] form) and `dense_decode` (the full read A for one decode query),
+both on the same kernel.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as nat
+
+TG = 256          # threads per block
+HEAD_DIM = 128    # 8 lanes x 16 dims
+MAX_H = 8
+MAX_P = 64        # partitions accepted by the MetalAttend-compatible entry point
+MAX_P_DENSE = 256
+
+
+def available() -> bool:
+    return nat.gpu_available()
+
+
+def _check_kv(KV, q, rows, partitions):
+    """Interleaved layout KV [G, C, 2*d] (metal_attend.py:177-189)."""
+    G, C, dd = KV.shape
+    if dd != 2 * HEAD_DIM:
+        raise ValueError("interleaved rows must hold K and V of head_dim 128")
+    h = int(q.shape[1]) if q.dim() == 3 else -1
+    if q.dim() != 3 or q.shape[0] != G or q.shape[2] != HEAD_DIM or q.dtype != torch.bfloat16 or not q.is_contiguous() \
+            or not 1 <= h <= MAX_H:
+        raise ValueError(f"q must be a contiguous bfloat16 [G, h, 128] tensor with h <= {MAX_H}")
+    if rows.dim() != 2 or rows.shape[0] != G or rows.dtype != torch.int32 or not rows.is_contiguous() or rows.shape[1] < 1:
+        raise ValueError("rows must be a contiguous int32 [G, S] tensor with S >= 1")
+    if not 1 <= int(partitions) <= MAX_P:
+        raise ValueError(f"partitions must be in [1, {MAX_P}]")
+    return G, C, h, int(rows.shape[1])
+
+
+def _check(K, V, q, rows, partitions):
+    """Separate-buffer layout K, V [G, C, d] (metal_attend.py:192-215)."""
+    if K.dim() != 3 or K.dtype != torch.bfloat16 or not K.is_contiguous():
+        raise ValueError("K must be a contiguous bfloat16 [G, C, d] tensor (batch 1)")
+    if V.shape != K.shape or V.dtype != torch.bfloat16 or not V.is_contiguous():
+        raise ValueError("V must match K")
+    G, C, d = K.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"head_dim must be {HEAD_DIM} (8 lanes x 16)")
+    if q.dim() != 3 or q.shape[0] != G or q.shape[2] != d or q.dtype != torch.bfloat16 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous bfloat16 [G, h, d] tensor")
+    h = int(q.shape[1])
+    if not 1 <= h <= MAX_H:
+        raise ValueError(f"h must be in [1, {MAX_H}]")
+    if rows.dim() != 2 or rows.shape[0] != G or rows.dtype != torch.int32 or not rows.is_contiguous():
+        raise ValueError("rows must be a contiguous int32 [G, S] tensor of original positions")
+    S = int(rows.shape[1])
+    if S < 1:
+        raise ValueError("at least one row must be selected")
+    if not 1 <= int(partitions) <= MAX_P:
+        raise ValueError(f"partitions must be in [1, {MAX_P}]")
+    for t in (V, q, rows):
+        if t.device != K.device:
+            raise ValueError("all inputs must live on the same device")
+    if not K.is_cuda:
+        raise ValueError("inputs must live on a HIP device")
+    return G, C, h, S
+
+
+def _out(out, shape, dtype, device):
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out_dtype must be float32 or bfloat16")
+    if out is None:
+        return torch.empty(*shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or not out.is_contiguous() or out.device != device:
+        raise ValueError(f"out must be a contiguous {dtype} tensor of shape {tuple(shape)}")
+    return out
+
+
+def _part(part, n, device):
+    if part is None:
+        return torch.empty(max(n, 1), dtype=torch.float32, device=device)
+    if part.dtype != torch.float32 or not part.is_contiguous() or part.numel() < n or part.device != device:
+        raise ValueError(f"part must be a contiguous float32 tensor of at least {n} elements")
+    return part
+
+
+class HipAttend:
+    """Gather-free subset attention: out[g, i] = softmax(q[g, i] . K[g, rows[g]] * scale) @ V[g, rows[g]]."""
+
+    def __init__(self):
+        if not available():
+            raise RuntimeError("needs a HIP device and the built libattnlab.so")
+
+    def __call__(self, K, V, q, rows, *, scale=None, partitions: int = 4, out_dtype=torch.float32, out=None, part=None,
+                 kv_interleaved=None):
+        """K, V [G, C, d] bf16; or `kv_interleaved` [G, C, 2, d] bf16 (K then V per position) with K and V ignored."""
+        if kv_interleaved is not None:
+            kv = kv_interleaved
+            if kv.dim() != 4 or kv.shape[2] != 2 or kv.dtype != torch.bfloat16 or not kv.is_contiguous():
+                raise ValueError("kv_interleaved must be a contiguous bfloat16 [G, C, 2, d] tensor")
+            base = kv.view(kv.shape[0], kv.shape[1], 2 * kv.shape[3])
+            G, C, h, S = _check_kv(base, q, rows, partitions)
+            if not base.is_cuda or q.device != base.device or rows.device != base.device:
+                raise ValueError("inputs must live on one HIP device")
+            k_ptr, v_ptr, row_stride = base.data_ptr(), base.data_ptr() + HEAD_DIM * 2, 2 * HEAD_DIM
+            device = base.device
+        else:
+            G, C, h, S = _check(K, V, q, rows, partitions)
+            k_ptr, v_ptr, row_stride = K.data_ptr(), V.data_ptr(), HEAD_DIM
+            device = K.device
+        P = int(partitions)
+        sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+        out = _out(out, (G, h, HEAD_DIM), out_dtype, device)
+        part = _part(part, G * P * h * (HEAD_DIM + 2) if P > 1 else 0, device)
+        nat.call("attnlab_attend", k_ptr, v_ptr, C * row_stride, row_stride, q.data_ptr(), rows.data_ptr(), S, 1, G, h,
+                 S, C, P, sc, out.data_ptr(), int(out.dtype == torch.bfloat16), part.data_ptr(), nat.stream_of(device))
+        return out
+
+
+def model_views(K4, V4, q5, rows3):
+    """Model-side tensors (batch 1) -> kernel views: K/V [G, C, d], q [G, h, d], rows int32 [G, S]."""
+    if K4.shape[0] != 1 or q5.shape[0] != 1 or rows3.shape[0] != 1:
+        raise ValueError("the batch-1 attend op takes batch 1 (use attend for batches)")
+    if q5.shape[3] != 1:
+        raise ValueError("one query position per step")
+    return K4[0], V4[0], q5[0, :, :, 0, :].contiguous(), rows3[0].to(torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# batched forms
+# ---------------------------------------------------------------------------------------------------------------------
+_SHARED_WS = nat.Workspace()
+
+
+def _check_cache(k, v, q):
+    if k.dim() != 4 or k.dtype != torch.bfloat16 or not k.is_contiguous() or not k.is_cuda:
+        raise ValueError("the cache must be a contiguous bfloat16 [B, G, C, d] tensor on a HIP device")
+    if v.shape != k.shape or v.dtype != k.dtype or not v.is_contiguous() or v.device != k.device:
+        raise ValueError("v must match k")
+    B, G, C, d = k.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"head_dim must be {HEAD_DIM}")
+    if q.dim() != 4 or tuple(q.shape[:2]) != (B, G) or q.shape[3] != d or q.dtype != torch.bfloat16 \
+            or not q.is_contiguous() or q.device != k.device:
+        raise ValueError("q must be a contiguous bfloat16 [B, G, h, d] tensor on the cache device")
+    h = int(q.shape[2])
+    if not 1 <= h <= MAX_H:
+        raise ValueError(f"h must be in [1, {MAX_H}]")
+    return B, G, C, h
+
+
+def auto_partitions(BG: int, rows: int, *, max_p: int, min_rows: int) -> int:
+    """Split-K count: enough blocks to cover the chip (~1024 blocks of 256 threads) with >= min_rows rows each."""
+    want = -(-1024 // max(BG, 1))
+    cap = max(1, rows // min_rows)
+    return max(1, min(max_p, want, cap))
+
+
+def attend(q, k, v, rows, *, scale=None, partitions=None, out=None, out_dtype=torch.bfloat16, workspace=None):
+    """Batched gather-free attention: q [B,G,h,d], k/v [B,G,C,d] bf16, rows int32 [B,G,S] -> out [B,G,h,d]."""
+    B, G, C, h = _check_cache(k, v, q)
+    if rows.dim() != 3 or tuple(rows.shape[:2]) != (B, G) or rows.dtype != torch.int32 or not rows.is_contiguous() \
+            or rows.device != k.device:
+        raise ValueError("rows must be a contiguous int32 [B, G, S] tensor on the cache device")
+    S = int(rows.shape[2])
+    if S < 1:
+        raise ValueError("at least one row must be selected")
+    P = auto_partitions(B * G, S, max_p=MAX_P, min_rows=64) if partitions is None else int(partitions)
+    if not 1 <= P <= MAX_P:
+        raise ValueError(f"partitions must be in [1, {MAX_P}]")
+    ws = _SHARED_WS if workspace is None else workspace
+    out = _out(out, (B, G, h, HEAD_DIM), out_dtype, k.device)
+    part = ws.bytes(k.device, B * G * P * h * (HEAD_DIM + 2) * 4, "attend_part") if P > 1 else None
+    sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    nat.call("attnlab_attend", k.data_ptr(), v.data_ptr(), C * HEAD_DIM, HEAD_DIM, q.data_ptr(), rows.data_ptr(), S,
+             B, G, h, S, C, P, sc, out.data_ptr(), int(out.dtype == torch.bfloat16), nat.ptr(part),
+             nat.stream_of(k.device))
+    return out
+
+
+def dense_decode(q, k, v, valid_length: int, *, scale=None, partitions=None, out=None, out_dtype=torch.bfloat16,
+                 workspace=None):
+    """Dense decode read A over positions [0, valid_length): q [B,G,h,d], k/v [B,G,C,d] -> out [B,G,h,d]."""
+    B, G, C, h = _check_cache(k, v, q)
+    L = int(valid_length)
+    if not 0 < L <= C:
+        raise ValueError(f"valid_length={L} must be in (0, capacity={C}]")
+    P = auto_partitions(B * G, L, max_p=MAX_P_DENSE, min_rows=256) if partitions is None else int(partitions)
+    if not 1 <= P <= MAX_P_DENSE:
+        raise ValueError(f"partitions must be in [1, {MAX_P_DENSE}]")
+    ws = _SHARED_WS if workspace is None else workspace
+    out = _out(out, (B, G, h, HEAD_DIM), out_dtype, k.device)
+    part = ws.bytes(k.device, B * G * P * h * (HEAD_DIM + 2) * 4, "dense_part") if P > 1 else None
+    sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    nat.call("attnlab_dense_decode", k.data_ptr(), v.data_ptr(), C * HEAD_DIM, HEAD_DIM, q.data_ptr(), B, G, h, L, C,
+             P, sc, out.data_ptr(), int(out.dtype == torch.bfloat16), nat.ptr(part), nat.stream_of(k.device))
+    return out

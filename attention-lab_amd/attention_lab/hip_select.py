@@ -1,0 +1,98 @@
+"""Top-k selection on gfx950 (the selection step the reference runs with torch.topk, decode.py:86-93).
+
+Order contract, defined where torch.topk leaves ties unspecified: a larger score ranks first, equal scores rank by the
+lower candidate index, NaN ranks below every number, -0.0 equals +0.0. `topk` returns (values, indices) like
+torch.topk(..., sorted=True) on the last dimension; `select_rows` writes the whole row list of a decode step
+(F merged with the chosen candidates) in the layout the attend kernel reads.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+MAX_SCORE_ORDER_K = 4096
+ORDERS = {"position": nat.ORDER_POSITION, "score": nat.ORDER_SCORE}
+
+
+def _order_code(order) -> int:
+    if order not in ORDERS:
+        raise ValueError(f"order must be one of {tuple(ORDERS)}, got {order!r}")
+    return ORDERS[order]
+
+
+def topk(scores, k: int, *, order: str = "score"):
+    """Top-k over the last dim of fp32 `scores` [..., M] -> (values fp32 [..., k], indices int64 [..., k]).
+
+    order="score": descending score, ties lowest index first (torch.topk's sorted order with ties defined);
+    order="position": the same set, indices ascending.
+    """
+    if scores.dtype != torch.float32 or not scores.is_cuda:
+        raise ValueError("scores must be a float32 tensor on a HIP device")
+    if scores.dim() < 1:
+        raise ValueError("scores must have at least one dimension")
+    code = _order_code(order)
+    M = int(scores.shape[-1])
+    k = int(k)
+    if not 0 <= k <= M:
+        raise ValueError(f"need 0 <= k <= {M}, got {k}")
+    if code == nat.ORDER_SCORE and k > MAX_SCORE_ORDER_K:
+        raise ValueError(f"score order supports k <= {MAX_SCORE_ORDER_K}")
+    lead = tuple(scores.shape[:-1])
+    s2 = scores.reshape(-1, M)
+    if s2.stride(-1) != 1:
+        s2 = s2.contiguous()
+    R = s2.shape[0]
+    idx = torch.empty(R, max(k, 1), dtype=torch.int32, device=scores.device)
+    val = torch.empty(R, max(k, 1), dtype=torch.float32, device=scores.device)
+    if R and k:
+        nat.call("attnlab_topk", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
+                 idx.stride(0), nat.stream_of(scores.device))
+    return val[:, :k].reshape(*lead, k), idx[:, :k].long().reshape(*lead, k)
+
+
+def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, order: str = "position",
+                rows=None, want_flat: bool = False):
+    """Row list of one decode step from candidate scores [B, G, hi-lo] (fp32, unit column stride).
+
+    Returns (rows int32 [B, G, S] original positions, flat int64 [B*G*S] row ids of the flattened cache or None),
+    S = lo + (legal - hi) + k. order="position" sorts every list ascending (canonical_order); order="score" puts F
+    first and then the candidates by descending score, like cat(fixed_rows, topk.indices) in decode.py:93.
+    """
+    if scores.dim() != 3 or scores.dtype != torch.float32 or not scores.is_cuda or scores.stride(2) != 1:
+        raise ValueError("scores must be a float32 [B, G, M] tensor with unit column stride on a HIP device")
+    B, G, M = scores.shape
+    lo, hi, legal, k, capacity = int(lo), int(hi), int(legal), int(k), int(capacity)
+    if M != hi - lo:
+        raise ValueError(f"scores hold {M} candidates but hi - lo = {hi - lo}")
+    if not 0 <= lo <= hi <= legal <= capacity:
+        raise ValueError(f"need 0 <= lo <= hi <= legal <= capacity, got {lo} {hi} {legal} {capacity}")
+    if not 0 <= k <= M:
+        raise ValueError(f"need 0 <= k <= {M}, got {k}")
+    code = _order_code(order)
+    S = lo + (legal - hi) + k
+    if rows is None:
+        rows = torch.empty(B, G, S, dtype=torch.int32, device=scores.device)
+    elif rows.dtype != torch.int32 or tuple(rows.shape) != (B, G, S) or not rows.is_contiguous():
+        raise ValueError(f"rows must be a contiguous int32 [{B}, {G}, {S}] tensor")
+    flat = torch.empty(B * G * S, dtype=torch.int64, device=scores.device) if want_flat else None
+    stride = row_stride(scores)
+    if stride is None:
+        scores = scores.contiguous()
+        stride = max(M, 1)
+    nat.call("attnlab_select_rows", scores.data_ptr(), stride, B, G, lo, hi, legal, k, capacity, code,
+             rows.data_ptr(), S, nat.ptr(flat), nat.stream_of(scores.device))
+    return rows, flat
+
+
+def row_stride(t3):
+    """Stride s such that row (b, g) of a [B, G, M] tensor starts at element (b*G + g) * s, or None."""
+    B, G, M = t3.shape
+    if t3.stride(2) != 1 and M > 1:
+        return None
+    if B * G == 1:
+        return max(M, 1)
+    s = t3.stride(1) if G > 1 else t3.stride(0)
+    if B > 1 and t3.stride(0) != G * s:
+        return None
+    return s if s >= M else None

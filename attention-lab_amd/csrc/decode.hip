@@ -1,0 +1,73 @@
+// One layer's sparse decode read as a single C-ABI call: score (z column + u + candidate scan) -> select (top-k + F
+// merge) -> gather-free attend, three launches on the caller's stream with the intermediate scores and row list in a
+// caller-provided workspace. Counterpart of sparse_decode_step_kernel (decode.py:145-163).
+#include "common.h"
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+
+inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct Layout {
+    int64_t scores, rows, part, total;
+    int64_t score_stride;
+};
+
+// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | partials [BG, P, h, 130] fp32.
+Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
+    Layout L{};
+    const int64_t BG = (int64_t)B * G;
+    const int64_t M = hi - lo;
+    const int64_t S = lo + (legal - hi) + k;
+    L.score_stride = (M + 3) / 4 * 4;
+    L.scores = 0;
+    L.rows = align_up(k > 0 ? BG * L.score_stride * 4 : 0);
+    L.part = L.rows + align_up(BG * S * 4);
+    L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
+    return L;
+}
+
+}  // namespace
+
+extern "C" int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
+    if (B < 1 || G < 1 || h < 1 || lo < 0 || hi < lo || legal < hi || k < 0 || P < 1) return -1;
+    return layout_of(B, G, h, lo, hi, legal, k, P).total;
+}
+
+extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K,
+                                          const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
+                                          const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
+                                          int legal, int k, int write_col, float scale, int order, int P,
+                                          void* workspace, int64_t workspace_bytes, int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
+    ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
+                    lo, hi, legal, C);
+    ATTNLAB_REQUIRE(0 <= k && k <= hi - lo, "need 0 <= k <= hi - lo, got k=%d M=%d", k, hi - lo);
+    ATTNLAB_REQUIRE(1 <= P && P <= 64, "partitions P=%d outside [1, 64]", P);
+    const Layout L = layout_of(B, G, h, lo, hi, legal, k, P);
+    ATTNLAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, "workspace of %lld bytes needed, got %lld",
+                    (long long)L.total, (long long)workspace_bytes);
+    ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, "workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    float* scores = reinterpret_cast<float*>(ws + L.scores);
+    int32_t* rows = rows_out ? rows_out : reinterpret_cast<int32_t*>(ws + L.rows);
+    float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
+    const int S = lo + (legal - hi) + k;
+    const int d = 128;
+    int rc;
+    if (k > 0) {
+        rc = attnlab_score_grouped(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, scores, L.score_stride, B, G, r, C, d,
+                                   h * d, lo, hi, write_col, 1, stream);
+    } else if (k_new) {
+        // no candidate is read this step, but the newest key still gets its index column (empty scan range)
+        rc = attnlab_score_grouped(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, nullptr, 0, B, G, r, C, d, h * d, lo, lo,
+                                   write_col, 1, stream);
+    } else {
+        rc = ATTNLAB_OK;
+    }
+    if (rc) return rc;
+    rc = attnlab_select_rows(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, stream);
+    if (rc) return rc;
+    return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
+}

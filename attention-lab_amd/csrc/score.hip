@@ -1,0 +1,420 @@
+// Index score kernels for gfx950.
+//
+// Grouped (parity) mode, the reference's indexer (src/attention_lab/indexer.py:15-29, metal_score.py:44-246):
+// one launch per decode step writes the z column of the newest key, builds u = q_cat . wq_t in fp32 and scans the
+// candidate columns of the transposed index table zT [B,G,r,C]. The table is column-contiguous for each j, so a
+// lane owns 8 adjacent columns and streams them with one 16-byte load per j (32 loads for r = 32): every wave load
+// is a 1 KiB contiguous run of HBM. The loads are issued before u is built, so the prologue (16-32 KiB of weights,
+// L2-resident after the first block) hides under the HBM latency instead of adding to it.
+//
+// Lightning mode (the north_star generalisation; no reference kernel): keys are stored one r-vector per position
+// [B,KG,Lk,r] (64 bytes of fp16/bf16 per position), four lanes share a position with 16 bytes each, the per-head
+// partial dot products are finished with two DPP quad steps, and ReLU and the head weights are applied in fp32.
+#include <algorithm>
+
+#include "common.h"
+
+namespace attnlab {
+
+struct ScoreArgs {
+    uint16_t* zT;           // [BG, r, C]
+    const uint16_t* k_new;  // [BG, d] or null
+    const uint16_t* wk;     // [G, r, d]
+    const uint16_t* q_cat;  // [BG, hd]
+    const uint16_t* wq_t;   // [G, hd, r]
+    const float* u_in;      // [BG, r] or null
+    float* u_out;           // [BG, r] or null
+    float* out;             // row bg at out + bg * out_stride
+    int64_t out_stride;
+    int G, r, C, d, hd, lo, M, write_col;
+    int tiles;              // column tiles per (b, g) row
+};
+
+constexpr int kMaxR = 32;
+
+// u[j] = sum_f q_cat[f] * wq_t[f, j] for one (b, g), reduced into u_sh[0..r). Uses `red` (BLOCK/64 x 32 floats).
+template <int BLOCK>
+__device__ __forceinline__ void build_u(const ScoreArgs& a, int bg, int g, float* u_sh, float* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint16_t* q = a.q_cat + (size_t)bg * a.hd;
+    const uint16_t* w = a.wq_t + (size_t)g * a.hd * a.r;
+    if (a.r == 32) {
+        // thread -> (feature stride BLOCK/4, j slice of 8): one 16-byte load covers 8 consecutive j of one feature
+        const int js = tid & 3;
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+        for (int f = tid >> 2; f < a.hd; f += BLOCK / 4) {
+            const float qf = bf16_to_f32(q[f]);
+            const uint4 wv = *reinterpret_cast<const uint4*>(w + (size_t)f * 32 + js * 8);
+            acc[0] += qf * bf16_lo(wv.x); acc[1] += qf * bf16_hi(wv.x);
+            acc[2] += qf * bf16_lo(wv.y); acc[3] += qf * bf16_hi(wv.y);
+            acc[4] += qf * bf16_lo(wv.z); acc[5] += qf * bf16_hi(wv.z);
+            acc[6] += qf * bf16_lo(wv.w); acc[7] += qf * bf16_hi(wv.w);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float v = acc[i];
+            v += shfl_xor_f32(v, 4);
+            v += shfl_xor_f32(v, 8);
+            v += shfl_xor_f32(v, 16);
+            v += shfl_xor_f32(v, 32);
+            acc[i] = v;
+        }
+        if (lane < 4) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red[wave * 32 + lane * 8 + i] = acc[i];
+        }
+    } else {
+        // general r <= 32: thread -> (j = tid % 32, feature stride BLOCK/32)
+        const int j = tid & 31;
+        float acc = 0.0f;
+        if (j < a.r)
+            for (int f = tid >> 5; f < a.hd; f += BLOCK / 32) acc += bf16_to_f32(q[f]) * bf16_to_f32(w[(size_t)f * a.r + j]);
+        acc += shfl_xor_f32(acc, 32);
+        if (lane < 32) red[wave * 32 + lane] = acc;
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < BLOCK / 64; ++w2) s += red[w2 * 32 + tid];
+        u_sh[tid] = (tid < a.r) ? s : 0.0f;
+        if (a.u_out && tid < a.r) a.u_out[(size_t)bg * a.r + tid] = s;
+    }
+}
+
+// z column of the newest key: zT[bg, j, write_col] = bf16_rne(wk[g, j, :] . k_new[bg, :]); 8 lanes per j.
+template <int BLOCK>
+__device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
+    const int tid = threadIdx.x;
+    const uint16_t* kn = a.k_new + (size_t)bg * a.d;
+    for (int j0 = 0; j0 < a.r; j0 += BLOCK / 8) {
+        const int j = j0 + (tid >> 3);
+        float s = 0.0f;
+        if (j < a.r) {
+            const uint16_t* wr = a.wk + ((size_t)g * a.r + j) * a.d;
+            for (int e = tid & 7; e < a.d; e += 8) s += bf16_to_f32(wr[e]) * bf16_to_f32(kn[e]);
+        }
+        s = sum8(s);
+        if ((tid & 7) == 0 && j < a.r) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = f32_to_bf16_rne(s);
+    }
+}
+
+// 16-byte-load scan: thread -> 8 adjacent columns starting at an 8-aligned column. Columns of the aligned group that
+// fall outside [lo, hi) are loaded (they lie inside the row because C % 8 == 0) but never stored.
+template <int BLOCK>
+__global__ __launch_bounds__(BLOCK) void score_scan_vec(ScoreArgs a) {
+    __shared__ float u_sh[32];
+    __shared__ float red[(BLOCK / 64) * 32];
+    const int bg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x;
+    const int hi = a.lo + a.M;
+    const int c0 = (a.lo & ~7) + (tile * BLOCK + tid) * 8;
+    const bool active = a.M > 0 && c0 < hi;
+    const uint16_t* col = a.zT + (size_t)bg * a.r * a.C + c0;
+
+    uint4 v[kMaxR];
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < kMaxR; ++j)
+            if (j < a.r) v[j] = *reinterpret_cast<const uint4*>(col + (size_t)j * a.C);
+    }
+    if (a.u_in) {
+        if (tid < 32) u_sh[tid] = tid < a.r ? a.u_in[(size_t)bg * a.r + tid] : 0.0f;
+    } else {
+        build_u<BLOCK>(a, bg, g, u_sh, red);
+    }
+    if (tile == 0 && a.k_new) write_z<BLOCK>(a, bg, g);
+    __syncthreads();
+    if (!active) return;
+
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxR; ++j) {
+        if (j < a.r) {
+            const float u = u_sh[j];
+            acc[0] += u * bf16_lo(v[j].x); acc[1] += u * bf16_hi(v[j].x);
+            acc[2] += u * bf16_lo(v[j].y); acc[3] += u * bf16_hi(v[j].y);
+            acc[4] += u * bf16_lo(v[j].z); acc[5] += u * bf16_hi(v[j].z);
+            acc[6] += u * bf16_lo(v[j].w); acc[7] += u * bf16_hi(v[j].w);
+        }
+    }
+    float* o = a.out + (size_t)bg * a.out_stride - a.lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = c0 + i;
+        if (c >= a.lo && c < hi) o[c] = acc[i];
+    }
+}
+
+// 2-byte-load scan for tables whose rows are not 16-byte aligned: thread -> 8 adjacent columns from lo, never
+// loading at or beyond hi.
+template <int BLOCK>
+__global__ __launch_bounds__(BLOCK) void score_scan_scalar(ScoreArgs a) {
+    __shared__ float u_sh[32];
+    __shared__ float red[(BLOCK / 64) * 32];
+    const int bg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x;
+    const int m0 = (tile * BLOCK + tid) * 8;
+    if (a.u_in) {
+        if (tid < 32) u_sh[tid] = tid < a.r ? a.u_in[(size_t)bg * a.r + tid] : 0.0f;
+    } else {
+        build_u<BLOCK>(a, bg, g, u_sh, red);
+    }
+    if (tile == 0 && a.k_new) write_z<BLOCK>(a, bg, g);
+    __syncthreads();
+    if (m0 >= a.M) return;
+    const int n = min(8, a.M - m0);
+    const uint16_t* col = a.zT + (size_t)bg * a.r * a.C + a.lo + m0;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < a.r; ++j) {
+        const float u = u_sh[j];
+        const uint16_t* row = col + (size_t)j * a.C;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i < n) acc[i] += u * bf16_to_f32(row[i]);
+    }
+    float* o = a.out + (size_t)bg * a.out_stride + m0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (i < n) o[i] = acc[i];
+}
+
+// u and the z column only, one block per (b, g).
+__global__ __launch_bounds__(256) void score_prologue(ScoreArgs a) {
+    __shared__ float u_sh[32];
+    __shared__ float red[4 * 32];
+    const int bg = blockIdx.x;
+    const int g = bg % a.G;
+    build_u<256>(a, bg, g, u_sh, red);
+    if (a.k_new) write_z<256>(a, bg, g);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Lightning mode. Block = 256 threads = 64 positions (4 lanes x 16 bytes each); q and w are staged in LDS.
+// ---------------------------------------------------------------------------------------------------------------
+struct LightningArgs {
+    const uint16_t* keys;  // [BKG, Lk, 32]
+    const float* q;        // [BKG, nh, 32]
+    const float* w;        // [BKG, nh]
+    float* out;
+    int64_t out_stride;
+    int Lk, nh, lo, M, relu, tiles;
+};
+
+template <bool F16, int NH>
+__global__ __launch_bounds__(256) void score_lightning(LightningArgs a) {
+    __shared__ float q_sh[NH][32];
+    __shared__ float w_sh[NH];
+    const int bkg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bkg * a.tiles;
+    const int tid = threadIdx.x;
+    const int quarter = tid & 3;                  // dims [8*quarter, 8*quarter + 8)
+    const int t = a.lo + tile * 64 + (tid >> 2);  // position
+    const bool ok = t < a.lo + a.M;
+    uint4 kv = make_uint4(0, 0, 0, 0);
+    if (ok) kv = *reinterpret_cast<const uint4*>(a.keys + ((size_t)bkg * a.Lk + t) * 32 + quarter * 8);
+    if (tid < NH * 32) {
+        const int i = tid >> 5;
+        q_sh[i][tid & 31] = i < a.nh ? a.q[((size_t)bkg * a.nh + i) * 32 + (tid & 31)] : 0.0f;
+    }
+    if (tid < NH) w_sh[tid] = tid < a.nh ? a.w[(size_t)bkg * a.nh + tid] : 0.0f;
+    __syncthreads();
+    float kf[8];
+    const uint32_t words[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (F16) {
+            kf[2 * i] = f16_to_f32((uint16_t)(words[i] & 0xffffu));
+            kf[2 * i + 1] = f16_to_f32((uint16_t)(words[i] >> 16));
+        } else {
+            kf[2 * i] = bf16_lo(words[i]);
+            kf[2 * i + 1] = bf16_hi(words[i]);
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NH; ++i) {
+        float dsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum += q_sh[i][quarter * 8 + e] * kf[e];
+        dsum += dpp_f32<0xB1>(dsum);
+        dsum += dpp_f32<0x4E>(dsum);
+        if (a.relu) dsum = fmaxf(dsum, 0.0f);
+        s += w_sh[i] * dsum;
+    }
+    if (ok && quarter == 0) a.out[(size_t)bkg * a.out_stride + (t - a.lo)] = s;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Bulk index-table build (prefill): zT[bg, j, col0 + t] = bf16_rne(wk[g, j, :] . k_pre[bg, t, :]) for t < T.
+// Block = 4 waves over 64 positions; lane = position, wave w owns j = w, w + 4, ...; the 64 key rows are staged in
+// LDS (row pitch 136 halves, so lanes reading their own row hit distinct banks) and wk rows are LDS broadcasts.
+// Stores of one j are 64 consecutive columns (128 bytes).
+// ---------------------------------------------------------------------------------------------------------------
+struct ProjectArgs {
+    const uint16_t* k_pre;  // row t of bg at k_pre + bg * k_bg_stride + t * k_row_stride
+    int64_t k_bg_stride, k_row_stride;
+    const uint16_t* wk;     // [G, r, d]
+    uint16_t* zT;           // [BG, r, C]
+    int G, T, r, d, C, col0, tiles;
+};
+
+constexpr int kProjPos = 64;
+constexpr int kProjPitch = 136;  // halves per staged key row (128 + 8 padding)
+
+__global__ __launch_bounds__(256) void project_keys_kernel(ProjectArgs a) {
+    __shared__ uint16_t ks[kProjPos * kProjPitch];
+    __shared__ uint16_t ws[kMaxR * 128];
+    const int bg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = tile * kProjPos;
+    // stage 64 key rows (d <= 128 halves each) with 16-byte loads: 16 lanes per row
+    for (int i = tid; i < kProjPos * 16; i += 256) {
+        const int row = i >> 4, seg = i & 15;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (t0 + row < a.T && seg * 8 < a.d)
+            v = *reinterpret_cast<const uint4*>(a.k_pre + (size_t)bg * a.k_bg_stride + (size_t)(t0 + row) * a.k_row_stride + seg * 8);
+        *reinterpret_cast<uint4*>(&ks[row * kProjPitch + seg * 8]) = v;
+    }
+    for (int i = tid; i < a.r * 16; i += 256) {
+        const int j = i >> 4, seg = i & 15;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (seg * 8 < a.d) v = *reinterpret_cast<const uint4*>(a.wk + ((size_t)g * a.r + j) * a.d + seg * 8);
+        *reinterpret_cast<uint4*>(&ws[j * 128 + seg * 8]) = v;
+    }
+    __syncthreads();
+    const int t = t0 + lane;
+    const uint32_t* krow = reinterpret_cast<const uint32_t*>(&ks[lane * kProjPitch]);
+    for (int j = wave; j < a.r; j += 4) {
+        const uint32_t* wrow = reinterpret_cast<const uint32_t*>(&ws[j * 128]);
+        float s = 0.0f;
+        for (int e2 = 0; e2 < a.d / 2; ++e2) {
+            const uint32_t kw = krow[e2], ww = wrow[e2];
+            s += bf16_lo(kw) * bf16_lo(ww);
+            s += bf16_hi(kw) * bf16_hi(ww);
+        }
+        if (t < a.T) a.zT[((size_t)bg * a.r + j) * a.C + a.col0 + t] = f32_to_bf16_rne(s);
+    }
+}
+
+}  // namespace attnlab
+
+using namespace attnlab;
+
+extern "C" int attnlab_project_keys(const uint16_t* k_pre, int64_t k_bg_stride, int64_t k_row_stride, const uint16_t* wk,
+                                    uint16_t* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && T >= 0, "B=%d G=%d T=%d out of range", B, G, T);
+    ATTNLAB_REQUIRE(r >= 1 && r <= kMaxR, "index width r=%d outside [1, %d]", r, kMaxR);
+    ATTNLAB_REQUIRE(d >= 2 && d <= 128 && d % 8 == 0, "head_dim d=%d must be a multiple of 8 in [8, 128]", d);
+    ATTNLAB_REQUIRE(0 <= col0 && col0 + T <= C, "columns [%d, %d) outside the table of C=%d", col0, col0 + T, C);
+    ATTNLAB_REQUIRE(k_pre && wk && zT, "k_pre, wk and zT must be device pointers");
+    ATTNLAB_REQUIRE(k_row_stride % 8 == 0 && k_bg_stride % 8 == 0 && reinterpret_cast<uintptr_t>(k_pre) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(wk) % 16 == 0,
+                    "k_pre rows and wk must be 16-byte aligned");
+    if (T == 0) return ATTNLAB_OK;
+    ProjectArgs a{k_pre, k_bg_stride, k_row_stride, wk, zT, G, T, r, d, C, col0, (T + kProjPos - 1) / kProjPos};
+    hipLaunchKernelGGL(project_keys_kernel, dim3(B * G * a.tiles), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    return check_launch("project_keys");
+}
+
+extern "C" int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                                     const uint16_t* wq_t, const float* u_in, float* u_out, float* out,
+                                     int64_t out_stride, int B, int G, int r, int C, int d, int hd, int lo, int hi,
+                                     int write_col, int vector, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
+    ATTNLAB_REQUIRE(r >= 1 && r <= kMaxR, "index width r=%d outside [1, %d]", r, kMaxR);
+    ATTNLAB_REQUIRE(C >= 1, "C=%d must be positive", C);
+    ATTNLAB_REQUIRE(k_new == nullptr || d >= 1, "writing the z column needs d >= 1, got %d", d);
+    ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= C, "need 0 <= lo <= hi <= C, got lo=%d hi=%d C=%d", lo, hi, C);
+    ATTNLAB_REQUIRE(zT != nullptr, "zT must be a device pointer");
+    ATTNLAB_REQUIRE(k_new == nullptr || wk != nullptr, "writing the z column needs wk");
+    ATTNLAB_REQUIRE(u_in != nullptr || (q_cat != nullptr && wq_t != nullptr && hd >= 1),
+                    "either u_in or (q_cat, wq_t, hd >= 1) is required");
+    if (k_new) {
+        ATTNLAB_REQUIRE(0 <= write_col && write_col < C, "write_col=%d outside [0, %d)", write_col, C);
+        ATTNLAB_REQUIRE(!(lo <= write_col && write_col < hi), "write_col=%d lies inside the scanned range [%d, %d)",
+                        write_col, lo, hi);
+    }
+    const int M = hi - lo;
+    ATTNLAB_REQUIRE(M == 0 || (out != nullptr && out_stride >= M), "out must hold M=%d scores per row", M);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    ScoreArgs a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 1};
+    const bool vec = vector && (C % 8 == 0) && (reinterpret_cast<uintptr_t>(zT) % 16 == 0);
+    // the r == 32 prologue reads wq_t with 16-byte loads
+    if (r == 32 && u_in == nullptr)
+        ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(wq_t) % 16 == 0, "wq_t must be 16-byte aligned");
+    const int BG = B * G;
+    if (M == 0) {
+        if (!k_new && !u_out) return ATTNLAB_OK;
+        hipLaunchKernelGGL(score_prologue, dim3(BG), dim3(256), 0, s, a);
+        return check_launch("score_prologue");
+    }
+    const int span = vec ? (((hi + 7) & ~7) - (lo & ~7)) : M;  // columns the threads cover
+    // 256-thread blocks cover 2048 columns; use 64-thread blocks (512 columns) when that gives too few blocks
+    const int tiles256 = (span + 2047) / 2048;
+    const bool small = (int64_t)BG * tiles256 < 512;
+    if (small) {
+        a.tiles = (span + 511) / 512;
+        if (vec) hipLaunchKernelGGL(score_scan_vec<64>, dim3(BG * a.tiles), dim3(64), 0, s, a);
+        else hipLaunchKernelGGL(score_scan_scalar<64>, dim3(BG * a.tiles), dim3(64), 0, s, a);
+    } else {
+        a.tiles = tiles256;
+        if (vec) hipLaunchKernelGGL(score_scan_vec<256>, dim3(BG * a.tiles), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(score_scan_scalar<256>, dim3(BG * a.tiles), dim3(256), 0, s, a);
+    }
+    return check_launch("score_scan");
+}
+
+extern "C" int attnlab_score_prologue(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                                      const uint16_t* wq_t, float* u_out, int B, int G, int r, int C, int d, int hd,
+                                      int write_col, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
+    ATTNLAB_REQUIRE(r >= 1 && r <= kMaxR, "index width r=%d outside [1, %d]", r, kMaxR);
+    ATTNLAB_REQUIRE(q_cat && wq_t && hd >= 1 && u_out, "q_cat, wq_t and u_out are required");
+    if (k_new) ATTNLAB_REQUIRE(zT && wk && 0 <= write_col && write_col < C, "write_col=%d outside [0, %d)", write_col, C);
+    if (r == 32) ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(wq_t) % 16 == 0, "wq_t must be 16-byte aligned");
+    ScoreArgs a{zT, k_new, wk, q_cat, wq_t, nullptr, u_out, nullptr, 0, G, r, C, d, hd, 0, 0, write_col, 1};
+    hipLaunchKernelGGL(score_prologue, dim3(B * G), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    return check_launch("score_prologue");
+}
+
+extern "C" int attnlab_score_lightning(const uint16_t* keys, int key_dtype, const float* q, const float* w, float* out,
+                                       int64_t out_stride, int B, int KG, int Lk, int r, int nh, int lo, int hi,
+                                       int relu, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && KG >= 1, "B and KG must be positive (B=%d KG=%d)", B, KG);
+    ATTNLAB_REQUIRE(r == 32, "lightning keys must have r == 32, got %d", r);
+    ATTNLAB_REQUIRE(nh >= 1 && nh <= 8, "index heads nh=%d outside [1, 8]", nh);
+    ATTNLAB_REQUIRE(key_dtype == ATTNLAB_DT_F16 || key_dtype == ATTNLAB_DT_BF16, "key dtype must be fp16 or bf16");
+    ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= Lk, "need 0 <= lo <= hi <= Lk, got lo=%d hi=%d Lk=%d", lo, hi, Lk);
+    ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 16 == 0, "keys must be 16-byte aligned");
+    const int M = hi - lo;
+    if (M == 0) return ATTNLAB_OK;
+    ATTNLAB_REQUIRE(out != nullptr && out_stride >= M, "out must hold M=%d scores per row", M);
+    LightningArgs a{keys, q, w, out, out_stride, Lk, nh, lo, M, relu, (M + 63) / 64};
+    const dim3 grid(B * KG * a.tiles);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool f16 = key_dtype == ATTNLAB_DT_F16;
+#define LAUNCH_LIGHTNING(NHV)                                                                           \
+    do {                                                                                                \
+        if (f16) hipLaunchKernelGGL((score_lightning<true, NHV>), grid, dim3(256), 0, s, a);           \
+        else hipLaunchKernelGGL((score_lightning<false, NHV>), grid, dim3(256), 0, s, a);              \
+    } while (0)
+    if (nh <= 1) LAUNCH_LIGHTNING(1);
+    else if (nh <= 2) LAUNCH_LIGHTNING(2);
+    else if (nh <= 4) LAUNCH_LIGHTNING(4);
+    else LAUNCH_LIGHTNING(8);
+#undef LAUNCH_LIGHTNING
+    return check_launch("score_lightning");
+}

@@ -1,0 +1,173 @@
+/*
+ * attnlab.h - C ABI of the MI355X (gfx950) sparse-decode hot path.
+ *
+ * Every entry point takes raw device pointers, plain integer shapes/strides and a hipStream_t (passed as void*),
+ * launches asynchronously on that stream, never synchronises and never allocates device memory. The return value
+ * is a status code:
+ *   ATTNLAB_OK (0)            work enqueued;
+ *   ATTNLAB_EINVAL (1)        an argument violates the contract (the Python layer raises ValueError);
+ *   ATTNLAB_ERUNTIME (2)      the HIP runtime reported an error (the Python layer raises RuntimeError).
+ * attnlab_last_error() returns a message for the last non-zero status of the calling thread.
+ *
+ * Tensor layouts follow the reference (paths relative to wlvh/attention-lab):
+ *   K, V cache       [B, G, C, d] bf16, row = one position (src/attention_lab/qwen_wrap.py:68-70)
+ *   index table zT   [B, G, r, C] (src/attention_lab/indexer.py:15-17, qwen_wrap.py:74-75)
+ *   query            [B, G, h, d] bf16 (q_main[B,G,h,1,d] of decode.py:145-147 with T == 1)
+ *   selection        F = [0, lo) U [hi, legal), candidates [lo, hi) (src/attention_lab/selection.py:69-86)
+ * bf16 and fp16 buffers are passed as uint16_t*. All pointers must be device pointers of the current device.
+ */
+#ifndef ATTNLAB_H
+#define ATTNLAB_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATTNLAB_OK 0
+#define ATTNLAB_EINVAL 1
+#define ATTNLAB_ERUNTIME 2
+
+/* Row-list order of attnlab_select_rows / attnlab_sparse_decode_step. */
+#define ATTNLAB_ORDER_POSITION 0 /* every row list ascending by position (canonical_order=True, decode.py:160-161) */
+#define ATTNLAB_ORDER_SCORE 1    /* F ascending, then the top-k by descending score, ties lowest index first
+                                    (cat(fixed_rows, topk.indices) of decode.py:86-93) */
+
+/* Index-key element types of the score kernels. */
+#define ATTNLAB_DT_BF16 0
+#define ATTNLAB_DT_F16 1
+#define ATTNLAB_DT_F32 2
+
+/* ABI version; bumped on any signature change. */
+int attnlab_abi_version(void);
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* attnlab_last_error(void);
+
+/* gfx target name of the device the library was built for ("gfx950"). */
+const char* attnlab_target(void);
+
+/*
+ * Grouped-indexer score, parity mode. Replaces MetalScore.fused / MetalScore.two_launch
+ * (src/attention_lab/metal_score.py:294-330, kernels :44-246) and, batched, the project_keys column write +
+ * project_queries + candidate_scores sequence of sparse_decode_step_kernel (decode.py:156-158, indexer.py:15-29).
+ *
+ * For every (b, g):
+ *   if k_new != NULL:  zT[b,g,j,write_col] = bf16_rne(sum_e wk[g,j,e] * k_new[b,g,e])          (j < r)
+ *   u[j]  = sum_f q_cat[b,g,f] * wq_t[g,f,j]   (fp32; 1/sqrt(r) is already folded into wq_t)   or u_in[b,g,j]
+ *   out[b,g,m] = sum_j u[j] * zT[b,g,j,lo+m]   (fp32) for m in [0, hi-lo)
+ * zT: [B,G,r,C] bf16 contiguous. k_new: [B,G,d] (nullable: no column write). wk: [G,r,d]. q_cat: [B,G,hd] with
+ * q_cat[f = i*d + e] = q_pre[b,g,i,e] (project_queries order). wq_t: [G,hd,r]. u_in: [B,G,r] fp32 (nullable; when
+ * given, q_cat/wq_t are not read). u_out: [B,G,r] fp32 (nullable; receives u). out: row (b,g) at out + bg*out_stride.
+ * Requires r <= 32, 0 <= lo <= hi <= C, 0 <= write_col < C and write_col outside [lo, hi) when k_new != NULL.
+ * vector != 0 selects the 16-byte-load scan (used when C % 8 == 0 and zT is 16-byte aligned; otherwise the 2-byte
+ * scan runs, the counterpart of the reference's v1 fallback, metal_score.py:289-292).
+ */
+int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                          const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride,
+                          int B, int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector,
+                          void* stream);
+
+/*
+ * Prologue only: u (and the z column when k_new != NULL). The first launch of MetalScore.two_launch
+ * (metal_score.py:314-321, kernel `prologue` :101-123). u_out: [B,G,r] fp32.
+ */
+int attnlab_score_prologue(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                           const uint16_t* wq_t, float* u_out, int B, int G, int r, int C, int d, int hd,
+                           int write_col, void* stream);
+
+/*
+ * Bulk index-table build: zT[b,g,j,col0+t] = bf16_rne(sum_e wk[g,j,e] * k_pre[b,g,t,e]) for t < T. Replaces
+ * project_keys (indexer.py:15-17) and the chunked table writes of the prefill (qwen_wrap.py:320-324).
+ * k_pre: row t of (b,g) at k_pre + bg*k_bg_stride + t*k_row_stride (elements, 16-byte aligned rows), d <= 128,
+ * d % 8 == 0. zT: [B,G,r,C] bf16. Requires 0 <= col0, col0 + T <= C.
+ */
+int attnlab_project_keys(const uint16_t* k_pre, int64_t k_bg_stride, int64_t k_row_stride, const uint16_t* wk,
+                         uint16_t* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream);
+
+/*
+ * Lightning-indexer score (no reference kernel: the generalisation north_star names; the grouped score of
+ * indexer.py:27-29 is the special case nh=1, w=1, relu=0, keys transposed):
+ *   out[b,kg,t] = sum_i w[b,kg,i] * act(sum_j q[b,kg,i,j] * key[b,kg,t,j])   for t in [lo, hi), act = ReLU or identity
+ * keys: [B,KG,Lk,r] (row layout, one r-vector per position) in key_dtype (ATTNLAB_DT_F16 or ATTNLAB_DT_BF16);
+ * q: [B,KG,nh,r] fp32; w: [B,KG,nh] fp32; out row (b,kg) at out + bkg*out_stride holds hi-lo fp32 scores.
+ * r must be 32; 1 <= nh <= 8.
+ */
+int attnlab_score_lightning(const uint16_t* keys, int key_dtype, const float* q, const float* w, float* out,
+                            int64_t out_stride, int B, int KG, int Lk, int r, int nh, int lo, int hi, int relu,
+                            void* stream);
+
+/*
+ * Top-k selection with lowest-index tie-break, no reference kernel (the reference calls torch.topk,
+ * decode.py:86-93 / :161-166; the planned P2 kernel was never built). For each of R rows of M fp32 scores
+ * (row i at scores + i*score_stride) selects the k largest; equal scores resolve to the lower index; NaN ranks below
+ * every number; -0.0 equals +0.0. Writes, when non-NULL, top_idx[i, 0..k) (int32 candidate-relative indices) and
+ * top_val[i, 0..k) (the scores), row stride top_stride, in `order`: ATTNLAB_ORDER_POSITION (ascending index) or
+ * ATTNLAB_ORDER_SCORE (descending score, then ascending index). Requires 0 <= k <= M.
+ */
+int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k, int order, int32_t* top_idx,
+                 float* top_val, int64_t top_stride, void* stream);
+
+/*
+ * Selection of one decode step: top-k over the candidate scores merged with the fixed set F, written as the row
+ * list the attend kernel reads. Replaces select_rows_kernel + the optional canonical sort
+ * (decode.py:86-93, :160-161) and DecodeRequest.select_positions (decode.py:50-56).
+ * scores: [B*G] rows of M = hi - lo candidate scores (row stride score_stride). F = [0, lo) U [hi, legal).
+ * S = lo + (legal - hi) + k. rows: [B*G, S] int32 positions (row stride rows_stride; nullable). rows_flat: [B*G*S]
+ * int64 flat row ids pos + (b*G+g)*C of the flattened [B*G*C, d] cache (sparse.py:14-16; nullable).
+ * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE (the latter needs k <= 4096).
+ */
+int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
+                        int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, void* stream);
+
+/*
+ * Gather-free sparse attention. Replaces MetalAttend.__call__ (metal_attend.py:226-250, kernels :46-169) and the
+ * index_select + subset SDPA of gathered_decode_step_kernel (decode.py:131-142, sparse.py:40-60):
+ *   out[b,g,i] = softmax_s(scale * q[b,g,i] . K[b,g,rows[b,g,s]]) @ V[b,g,rows[b,g,s]]   over s < S
+ * K/V: position p of (b,g) at K + bg*kv_bg_stride + p*kv_row_stride (elements; V likewise), d = 128 contiguous
+ * values per position. The interleaved diagnostic layout [G,C,2,d] is K = base, V = base + 128, row stride 256.
+ * q: [B,G,h,128] bf16 contiguous, 1 <= h <= 8. rows: [B*G, S] int32 positions (row stride rows_stride), S >= 1,
+ * positions outside [0, C) are skipped (never read). P split-K partitions (1..256); when P > 1, part must hold
+ * B*G*P*h*130 floats and a second small kernel merges the partials. out: [B,G,h,128], bf16 (RNE) when out_bf16
+ * else fp32.
+ */
+int attnlab_attend(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                   const uint16_t* q, const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int C,
+                   int P, float scale, void* out, int out_bf16, float* part, void* stream);
+
+/*
+ * Dense decode attention over positions [0, L): the control read A. Replaces full_attention(backend="sdpa_fold")
+ * for one decode query at the last legal position (full.py:17-34) and dense_decode_step (decode.py:174-176).
+ * Same layouts and partials contract as attnlab_attend.
+ */
+int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                         const uint16_t* q, int B, int G, int h, int L, int C, int P, float scale, void* out,
+                         int out_bf16, float* part, void* stream);
+
+/*
+ * Workspace (bytes) of attnlab_sparse_decode_step for these sizes: candidate scores, row list and split-K
+ * partials, each 256-byte aligned.
+ */
+int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int legal, int k, int P);
+
+/*
+ * One layer's sparse decode read for one new query: z column write, u projection, candidate scan, top-k, merge with
+ * F, gather-free attention. Replaces sparse_decode_step_kernel (decode.py:145-163) with three launches on `stream`.
+ * q_main: [B,G,h,128] bf16 (post-RoPE query); q_cat: [B,G,h*128] bf16 (pre-RoPE query, project_queries order);
+ * K/V: [B,G,C,128] bf16; zT: [B,G,r,C] bf16; wq_t: [G,h*128,r]; wk: [G,r,128]; k_new: [B,G,128] (nullable: the
+ * z column is not written). F = [0, lo) U [hi, legal); k top candidates; write_col = legal - 1 for the reference's
+ * plan. rows_out: [B*G, S] int32 positions (nullable: kept in the workspace); rows_flat: [B*G*S] int64 flat ids
+ * (nullable). out: [B,G,h,128] bf16. P: split-K partitions of the attend (1..64). order as in attnlab_select_rows.
+ */
+int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K, const uint16_t* V,
+                               uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk, const uint16_t* k_new,
+                               int B, int G, int h, int r, int C, int lo, int hi, int legal, int k, int write_col,
+                               float scale, int order, int P, void* workspace, int64_t workspace_bytes,
+                               int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATTNLAB_H */

@@ -1,0 +1,72 @@
+"""The C ABI: header, binding and library agree; argument validation runs on the host (no GPU, no compute call)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from attention_lab import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "attnlab.h"
+
+
+def header_symbols():
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\*?\s+\*?(attnlab_[a-z0-9_]+)\s*\(", text, flags=re.M))
+
+
+def header_arity(name):
+    text = " ".join(HEADER.read_text().split())
+    m = re.search(rf"\b{name}\s*\(([^)]*)\)\s*;", text)
+    assert m, name
+    args = m.group(1).strip()
+    return 0 if args in ("", "void") else len(args.split(","))
+
+
+def test_header_and_binding_declare_the_same_entry_points():
+    syms = header_symbols()
+    assert syms == set(_native.SIGNATURES), syms ^ set(_native.SIGNATURES)
+    for name, (_, args) in _native.SIGNATURES.items():
+        assert header_arity(name) == len(args), f"{name}: header has {header_arity(name)} args, binding {len(args)}"
+
+
+def test_library_exports_every_declared_symbol(native_lib):
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    for name in header_symbols():
+        assert hasattr(lib, name), f"libattnlab.so does not export {name}"
+    assert native_lib.attnlab_abi_version() == _native.ABI_VERSION
+    assert native_lib.attnlab_target() == b"gfx950"
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(native_lib):
+    """These calls fail validation on the host; no device pointer is touched and no kernel is launched."""
+    with pytest.raises(ValueError, match="k <= M"):
+        _native.call("attnlab_topk", None, 10, 1, 10, 11, 0, None, None, 11, None)
+    with pytest.raises(ValueError, match="write_col"):
+        _native.call("attnlab_score_grouped", 16, 16, 16, 16, 16, None, None, 16, 100, 1, 8, 32, 128, 128, 256, 4, 100,
+                     50, 1, None)
+    with pytest.raises(ValueError, match="index width"):
+        _native.call("attnlab_score_grouped", 16, None, 16, 16, 16, None, None, 16, 100, 1, 8, 33, 128, 128, 256, 4, 100,
+                     120, 1, None)
+    with pytest.raises(ValueError, match="h=9"):
+        _native.call("attnlab_attend", 16, 16, 128 * 128, 128, 16, 16, 10, 1, 8, 9, 10, 128, 1, 0.1, 16, 1, None, None)
+    with pytest.raises(ValueError, match="partitions"):
+        _native.call("attnlab_dense_decode", 16, 16, 128 * 128, 128, 16, 1, 8, 2, 10, 128, 0, 0.1, 16, 1, None, None)
+    with pytest.raises(ValueError, match="legal"):
+        _native.call("attnlab_select_rows", 16, 10, 1, 8, 4, 20, 10, 3, 100, 0, 16, 10, None, None)
+    with pytest.raises(ValueError, match="workspace"):
+        _native.call("attnlab_sparse_decode_step", *([16] * 8), 1, 8, 2, 32, 4096, 4, 4032, 4096, 128, 4095, 0.1, 0, 4,
+                     256, 10, None, None, 16, None)
+
+
+def test_workspace_size_formula(native_lib):
+    def expect(B, G, h, lo, hi, legal, k, P):
+        a = lambda x: (x + 255) // 256 * 256  # noqa: E731
+        BG, M, S = B * G, hi - lo, lo + (legal - hi) + k
+        scores = a(BG * ((M + 3) // 4 * 4) * 4) if k > 0 else 0
+        return scores + a(BG * S * 4) + (a(BG * P * h * 130 * 4) if P > 1 else 0)
+    for args in ((16, 8, 4, 4, 32704, 32768, 1024, 4), (1, 8, 2, 4, 1984, 2048, 64, 1), (2, 8, 2, 60, 60, 60, 0, 8)):
+        assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)
+    assert native_lib.attnlab_sparse_decode_workspace(0, 8, 2, 4, 100, 164, 3, 1) == -1

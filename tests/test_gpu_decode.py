@@ -1,0 +1,219 @@
+"""The whole sparse decode step (z column -> score -> top-k -> row list -> gather-free attend) against the oracle.
+
+Bars: row lists bit-exact against the oracle's top-k on the kernel's own fp32 scores; scores within 1e-5 of the
+float64 oracle; z column >= 99% bitwise equal to the RNE of the exact value; attention output within north_star's bf16
+tolerance (max |d| <= 2e-2, mean |d| <= 2e-3) of the float64 subset attention over the same rows. Invariants from the
+reference's contracts: NaN poison in unselected or unwritten rows is inert, every candidate selected (k = M) equals
+the dense read, legal <= 68 degenerates to the dense read, rows are original positions.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from attention_lab import hip_attend, hip_score, hip_select
+from attention_lab.decode import (dense_decode_step, gathered_decode_step_kernel, prepare_request,
+                                  select_rows_kernel, sparse_decode_step, sparse_decode_step_kernel)
+from attention_lab.indexer import GroupedIndexer
+from oracle import bf16, exact, rules
+
+pytestmark = pytest.mark.gpu
+f64 = bf16.values
+BF16_MAX, BF16_MEAN = 2e-2, 2e-3
+
+
+def setup(gpu, B=1, G=8, h=2, C=2048 + 64, seed=0, r=32):
+    gen = torch.Generator().manual_seed(seed)
+    t = lambda *s: torch.randn(*s, generator=gen).to(torch.bfloat16).to(gpu)  # noqa: E731
+    K, V = t(B, G, C, 128), t(B, G, C, 128)
+    q, q_pre, k_pre_new = t(B, G, h, 1, 128), t(B, G, h, 1, 128), t(B, G, 1, 128)
+    zT = t(B, G, r, C)
+    idx = GroupedIndexer(G, h, 128, r, device=gpu, dtype=torch.bfloat16, seed=seed)
+    return K, V, q, q_pre, k_pre_new, zT, idx
+
+
+def run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical, n0=None):
+    B, G, C = K.shape[0], K.shape[1], K.shape[2]
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu, n0=n0)
+    out, rows = sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo,
+                                          req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count,
+                                          k_pre_new=k_pre_new, write_col=req.write_col, return_rows=True,
+                                          canonical_order=canonical)
+    torch.cuda.synchronize()
+    pos = (rows.view(B, G, -1) - req.offsets).cpu().numpy()
+    return req, out, pos
+
+
+def kernel_scores(zT, q_pre, idx, lo, hi):
+    B, G, h, _, d = q_pre.shape
+    s = hip_score.score_grouped(zT, lo, hi, q_cat=q_pre.reshape(B, G, h * d).contiguous(), wq_t=idx.wq_t_scaled)
+    torch.cuda.synchronize()
+    return s.cpu().numpy()
+
+
+def check_out(out, ref, what):
+    o = f64(out).reshape(ref.shape)
+    d = np.abs(o - ref)
+    assert d.max() <= BF16_MAX and d.mean() <= BF16_MEAN, f"{what}: max {d.max():.3e} mean {d.mean():.3e}"
+
+
+@pytest.mark.parametrize("B,h,C,L,rho,canonical", [
+    (1, 2, 2048 + 64, 2048, 1 / 32, True),      # config 1: k = 64, S = 132
+    (1, 2, 2048 + 64, 2048, 1 / 32, False),
+    (2, 4, 3000, 2900, 1 / 8, True),
+    (1, 2, 300, 256, 1 / 8, False),             # (lo, hi, k) = (4, 192, 32)
+    (1, 2, 200, 128, 1 / 8, True),              # (68, 16, 84)
+    (3, 1, 1000, 1000, 1 / 32, False),
+])
+def test_step_matches_oracle(gpu, B, h, C, L, rho, canonical):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L)
+    zT_before = zT.clone()
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical)
+    lo, hi, k, S = rules.step(L, req.k0)
+    assert (req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count) == (lo, hi, k, S)
+    assert pos.shape == (B, 8, S)
+    # z column written, nothing else
+    z, z_bits = exact.z_column(f64(k_pre_new).reshape(B, 8, 128), f64(idx.wk))
+    assert np.mean(bf16.from_torch(zT[..., L - 1]) == z_bits) >= 0.99
+    mask = torch.ones(C, dtype=torch.bool, device=gpu)
+    mask[L - 1] = False
+    assert torch.equal(zT[..., mask], zT_before[..., mask])
+    # scores within 1e-5 of the oracle; rows bit-exact against the oracle's selection on those scores
+    s = kernel_scores(zT, q_pre, idx, lo, hi)
+    u = exact.grouped_u(f64(q_pre).reshape(B, 8, h * 128), f64(idx.wq_t_scaled))
+    assert np.abs(s - exact.grouped_scores(u, f64(zT), lo, hi)).max() <= 1e-5
+    want = exact.select_rows(s, lo, hi, L, k, order="position" if canonical else "score")
+    assert np.array_equal(pos, want), "row list differs from the oracle"
+    ref = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), want)
+    check_out(out, ref, "sparse step")
+
+
+def test_every_candidate_selected_equals_dense(gpu):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=2, C=1200, seed=9)
+    L = 1100
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, 1.0, True)
+    assert req.selected_count == L
+    assert np.array_equal(pos, np.broadcast_to(np.arange(L), pos.shape))
+    dense = dense_decode_step(q, K, V, L)
+    torch.cuda.synchronize()
+    assert float((out.float() - dense.float()).abs().max()) <= 1e-2
+    check_out(out, exact.dense_attention(f64(q)[:, :, :, 0], f64(K), f64(V), L), "k = M vs dense")
+
+
+@pytest.mark.parametrize("L,rho,k_expect,S_expect", [(60, 1 / 8, 0, 60), (128, 0.0, 0, 68), (40, 1.0, 0, 40)])
+def test_short_history_and_zero_budget(gpu, L, rho, k_expect, S_expect):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, C=256, seed=L)
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, False)
+    assert (req.k, req.selected_count) == (k_expect, S_expect)
+    assert np.array_equal(pos[0, 0], np.array(rules.fixed_positions(L)))
+    ref = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), pos)
+    check_out(out, ref, "F only")
+    _, z_bits = exact.z_column(f64(k_pre_new).reshape(1, 8, 128), f64(idx.wk))
+    assert np.mean(bf16.from_torch(zT[..., L - 1]) == z_bits) >= 0.99
+
+
+def test_k0_fixed_by_n0_then_clamped(gpu):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, C=128, seed=1)
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, 100, 1 / 32, True, n0=8192)
+    assert (req.k0, req.k, req.selected_count) == (256, 32, 100)
+    assert np.array_equal(pos[0, 0], np.arange(100))
+
+
+def test_poisoned_unselected_and_unwritten_rows_are_inert(gpu):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, C=2304, seed=4)
+    L = 2200
+    zc = zT.clone()
+    _, clean, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zc, idx, L, 1 / 16, True)
+    Kp, Vp, zp = K.clone(), V.clone(), zT.clone()
+    for g in range(8):
+        keep = torch.zeros(2304, dtype=torch.bool)
+        keep[torch.from_numpy(pos[0, g])] = True
+        Kp[0, g, ~keep.to(gpu)] = float("nan")
+        Vp[0, g, ~keep.to(gpu)] = float("nan")
+    zp[..., L:] = float("nan")                                     # unwritten index columns
+    zp[..., L - 1] = float("nan")                                  # the column the step writes
+    _, poisoned, pos2 = run_step(gpu, Kp, Vp, q, q_pre, k_pre_new, zp, idx, L, 1 / 16, True)
+    assert np.array_equal(pos, pos2)
+    assert bool(torch.isfinite(poisoned.float()).all()), "D read a row it did not select"
+    assert torch.equal(poisoned, clean)
+    dense = dense_decode_step(q, Kp, Vp, L)
+    torch.cuda.synchronize()
+    assert not bool(torch.isfinite(dense.float()).all()), "the dense read must see the poison"
+
+
+def test_reference_api_paths(gpu):
+    """select_rows_kernel / gathered_decode_step_kernel / DecodeRequest / sparse_decode_step agree with the fused step."""
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=2, C=1100, seed=5)
+    L = 1024
+    req = prepare_request(2, 8, 1100, valid_length=L, query_position=L - 1, rho=1 / 8, device=gpu)
+    z1 = zT.clone()
+    out_a = sparse_decode_step(q, q_pre, K, V, z1, idx, req, k_pre_new=k_pre_new)
+    u = idx.query(q_pre)
+    rows = select_rows_kernel(u, z1, req.fixed_rows, req.off_lo, req.layout.candidate_lo, req.layout.candidate_hi, req.k)
+    pos_sel = req.select_positions(u, z1)
+    out_b = gathered_decode_step_kernel(q, K, V, rows, req.selected_count)
+    torch.cuda.synchronize()
+    assert torch.equal((rows.view(2, 8, -1) - req.offsets), pos_sel), "row ids and positions disagree"
+    assert torch.equal(out_a, out_b)
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    s = kernel_scores(z1, q_pre, idx, lo, hi)
+    assert np.array_equal(pos_sel.cpu().numpy(), exact.select_rows(s, lo, hi, L, req.k, order="score"))
+    top = pos_sel[..., req.layout.fixed_count:]
+    assert bool(((top >= lo) & (top < hi)).all()), "chosen candidates must stay inside the candidate domain"
+
+
+def test_full_size_32k_b16_properties(gpu):
+    """C5 attention geometry at one layer: B=16, 32K, 8 KV groups, h=4, rho=1/32 -> k=1024, S=1092."""
+    B, G, h, L = 16, 8, 4, 32768
+    C = L
+    dev = gpu
+    torch.manual_seed(0)
+    K = torch.randn(B, G, C, 128, device=dev, dtype=torch.bfloat16)
+    V = torch.randn(B, G, C, 128, device=dev, dtype=torch.bfloat16)
+    zT = torch.randn(B, G, 32, C, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(B, G, h, 1, 128, device=dev, dtype=torch.bfloat16)
+    q_pre = torch.randn(B, G, h, 1, 128, device=dev, dtype=torch.bfloat16)
+    k_pre_new = torch.randn(B, G, 1, 128, device=dev, dtype=torch.bfloat16)
+    idx = GroupedIndexer(G, h, 128, 32, device=dev, dtype=torch.bfloat16, seed=0)
+    req, out, pos = run_step(dev, K, V, q, q_pre, k_pre_new, zT, idx, L, 1 / 32, True)
+    assert (req.k, req.selected_count) == (1024, 1092)
+    assert np.all(np.diff(pos, axis=-1) > 0), "canonical rows must be strictly ascending (sorted, unique)"
+    assert pos.min() >= 0 and pos.max() < L
+    fixed = np.array(rules.fixed_positions(L))
+    assert np.array_equal(pos[..., :4], np.broadcast_to(fixed[:4], (B, G, 4)))
+    assert np.array_equal(pos[..., -64:], np.broadcast_to(fixed[4:], (B, G, 64)))
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    s = kernel_scores(zT, q_pre, idx, lo, hi)
+    assert np.array_equal(pos, exact.select_rows(s, lo, hi, L, 1024, order="position"))
+    ref = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), pos)
+    check_out(out, ref, "32K B16")
+
+
+def test_graph_replay_matches_eager(gpu):
+    """The three launches of a step captured in a HIP graph: every replay equals the eager result."""
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=4, h=4, C=4096, seed=8)
+    L = 4000
+    req = prepare_request(4, 8, 4096, valid_length=L, query_position=L - 1, rho=1 / 32, device=gpu)
+    args = (q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo, req.layout.candidate_lo,
+            req.layout.candidate_hi, req.k, req.selected_count)
+    kw = dict(k_pre_new=k_pre_new, write_col=req.write_col, canonical_order=True)
+    eager = sparse_decode_step_kernel(*args, **kw).clone()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        sparse_decode_step_kernel(*args, **kw)                      # warm the workspace on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured = sparse_decode_step_kernel(*args, **kw)
+    for _ in range(3):
+        captured.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        dense_decode_step(q, K, V, L)                               # eager work between replays
+        torch.cuda.synchronize()

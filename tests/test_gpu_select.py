@@ -1,0 +1,120 @@
+"""Top-k / row-list kernel on the GPU against the oracle's deterministic top-k: index sets and orders bit-exact.
+
+The reference uses torch.topk (decode.py:86-93) and checks only set equality against a float64 brute force on tie-free
+scores (test_attention_contracts.py:254-277). Given identical fp32 scores, this kernel must return exactly the oracle's
+indices, including the order contract for ties (lower index first), NaN (never before a number) and -0.0 == +0.0.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from attention_lab import hip_select
+from oracle import exact
+
+pytestmark = pytest.mark.gpu
+
+
+def heavy_tail(R, M, seed, frac=0.02, sigma=3.0):
+    """Config 2 scores: N(0,1) with 2% of positions lifted by +3 sigma (seeded)."""
+    rng = np.random.default_rng(seed)
+    s = rng.standard_normal((R, M)).astype(np.float32)
+    n = max(1, int(frac * M))
+    for i in range(R):
+        idx = rng.choice(M, size=n, replace=False)
+        s[i, idx] += np.float32(sigma * s[i].std())
+    return s
+
+
+def check_topk(gpu, s: np.ndarray, k: int):
+    t = torch.from_numpy(s).to(gpu)
+    for order in ("score", "position"):
+        if order == "score" and k > hip_select.MAX_SCORE_ORDER_K:
+            continue
+        vals, idx = hip_select.topk(t, k, order=order)
+        torch.cuda.synchronize()
+        want = exact.topk(s, k, order=order)
+        got = idx.cpu().numpy()
+        assert np.array_equal(got, want), f"order={order} M={s.shape[-1]} k={k}: indices differ"
+        np.testing.assert_array_equal(vals.cpu().numpy(), np.take_along_axis(s, want, -1))
+
+
+@pytest.mark.parametrize("M", [1, 5, 100, 1000, 4093, 32700, 32768, 40000, 65468, 131008])
+def test_topk_matches_oracle_heavy_tail(gpu, M):
+    R = 4 if M > 40000 else 8
+    s = heavy_tail(R, M, seed=M)
+    for k in sorted({0, 1, max(1, M // 32), min(M, 4096), M}):
+        check_topk(gpu, s, k)
+
+
+@pytest.mark.parametrize("M,k", [(32700, 1024), (65468, 2046), (131008, 4094)])
+def test_topk_position_order_large_k(gpu, M, k):
+    s = heavy_tail(2, M, seed=k)
+    t = torch.from_numpy(s).to(gpu)
+    _, idx = hip_select.topk(t, k, order="position")
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy(), exact.topk(s, k, order="position"))
+
+
+def test_ties_resolve_to_the_lowest_index(gpu):
+    rng = np.random.default_rng(7)
+    for M, levels in ((1000, 3), (5000, 17), (32700, 50)):
+        s = (rng.integers(0, levels, size=(6, M)) * 0.5).astype(np.float32)
+        s[0] = 1.0                                                   # every score equal
+        for k in (1, 7, M // 32, M // 2):
+            check_topk(gpu, s, k)
+
+
+def test_nan_signed_zero_and_infinities(gpu):
+    rng = np.random.default_rng(3)
+    M = 3000
+    s = rng.standard_normal((4, M)).astype(np.float32)
+    s[0, ::7] = np.nan
+    s[1, :] = 0.0
+    s[1, ::2] = -0.0                                                 # -0.0 ties with +0.0 by index
+    s[2, ::5] = np.inf
+    s[2, 1::5] = -np.inf
+    s[3, :] = np.nan
+    s[3, 10:20] = -np.inf
+    for k in (1, 50, 500, M - 1, M):
+        for order in ("score", "position"):
+            if k > 4096:
+                continue
+            t = torch.from_numpy(s).to(gpu)
+            _, idx = hip_select.topk(t, k, order=order)
+            torch.cuda.synchronize()
+            assert np.array_equal(idx.cpu().numpy(), exact.topk(s, k, order=order)), (k, order)
+
+
+@pytest.mark.parametrize("legal,k0,order", [(2048, 64, "position"), (2048, 64, "score"), (300, 37, "score"),
+                                            (60, 10, "position"), (32768, 1024, "position"), (32768, 1024, "score"),
+                                            (100, 0, "score"), (1000, 932, "position")])
+def test_select_rows_matches_oracle(gpu, legal, k0, order):
+    from oracle import rules
+    B, G = 2, 8
+    lo, hi, k, S = rules.step(legal, k0)
+    C = legal + 40
+    s = heavy_tail(B * G, max(hi - lo, 1), seed=legal + k0)[:, :hi - lo].reshape(B, G, hi - lo)
+    t = torch.from_numpy(np.ascontiguousarray(s)).to(gpu)
+    rows, flat = hip_select.select_rows(t, lo, hi, legal, k, C, order=order, want_flat=True)
+    torch.cuda.synchronize()
+    want = exact.select_rows(s, lo, hi, legal, k, order=order)
+    assert rows.shape == (B, G, S)
+    assert np.array_equal(rows.cpu().numpy(), want)
+    off = (np.arange(B * G) * C).reshape(B, G, 1)
+    assert np.array_equal(flat.cpu().numpy().reshape(B, G, S), want + off)
+
+
+def test_validation(gpu):
+    t = torch.zeros(2, 100, device=gpu)
+    with pytest.raises(ValueError):
+        hip_select.topk(t, 101)
+    with pytest.raises(ValueError):
+        hip_select.topk(t.double(), 3)
+    with pytest.raises(ValueError):
+        hip_select.topk(torch.zeros(2, 10000, device=gpu), 5000, order="score")
+    with pytest.raises(ValueError):
+        hip_select.topk(t, 3, order="random")
+    with pytest.raises(ValueError):
+        hip_select.select_rows(torch.zeros(1, 8, 10, device=gpu), 4, 15, 20, 3, 32)   # M != hi - lo
