@@ -15,7 +15,8 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
+HIST_BINS = 2048   # first radix digit of the top-k: top 11 bits of the order-preserving score key
 
 ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2
 ORDER_POSITION, ORDER_SCORE = 0, 1
@@ -28,16 +29,16 @@ SIGNATURES = {
     "attnlab_abi_version": (_i, []),
     "attnlab_last_error": (ctypes.c_char_p, []),
     "attnlab_target": (ctypes.c_char_p, []),
-    "attnlab_score_grouped": (_i, [_p] * 8 + [_i64] + [_i] * 10 + [_p]),
+    "attnlab_score_grouped": (_i, [_p] * 8 + [_i64] + [_i] * 10 + [_p, _p]),
     "attnlab_score_prologue": (_i, [_p] * 6 + [_i] * 7 + [_p]),
     "attnlab_project_keys": (_i, [_p, _i64, _i64, _p, _p] + [_i] * 7 + [_p]),
     "attnlab_score_lightning": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 8 + [_p]),
     "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
-    "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p]),
+    "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
-    "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _i64, _p, _p, _p, _p]),
+    "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()
@@ -105,10 +106,12 @@ def ptr(t) -> int | None:
 
 
 class Workspace:
-    """Growable device scratch owned by one op object (split-K partials, intermediate scores and row lists).
+    """Growable device scratch owned by one op object (split-K partials, intermediate scores, row lists, top-k
+    histograms).
 
-    Two launches that share one Workspace must be ordered on one stream. Grow it (one eager call) before capturing
-    the launches in a HIP graph, so no allocation happens under capture.
+    Buffers are zero-filled when allocated: the top-k histograms must start at zero, and the kernels leave them
+    zeroed after every call. Two launches that share one Workspace must be ordered on one stream. Grow it (one eager
+    call) before capturing the launches in a HIP graph, so no allocation happens under capture.
     """
 
     def __init__(self):
@@ -118,6 +121,6 @@ class Workspace:
         key = (device, tag)
         buf = self._bytes.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
             self._bytes[key] = buf
         return buf

@@ -86,7 +86,7 @@ class HipScore:
         out = _out_buffer(out, G, M, zT.device)
         nat.call("attnlab_score_grouped", zT.data_ptr(), k_new.data_ptr(), wk.data_ptr(), q_cat.data_ptr(),
                  wq_t.data_ptr(), None, None, out.data_ptr(), out.stride(0), 1, G, r, C, d, hd, lo, hi, write_col,
-                 int(version == 2), nat.stream_of(zT.device))
+                 int(version == 2), None, nat.stream_of(zT.device))
         return out[:, :M]
 
     def two_launch(self, zT, k_new, wk, q_cat, wq_t, lo: int, hi: int, write_col: int, out=None, u_buf=None,
@@ -104,7 +104,7 @@ class HipScore:
                  wq_t.data_ptr(), u_buf.data_ptr(), 1, G, r, C, d, hd, write_col, s)
         if M > 0:
             nat.call("attnlab_score_grouped", zT.data_ptr(), None, wk.data_ptr(), None, None, u_buf.data_ptr(), None,
-                     out.data_ptr(), out.stride(0), 1, G, r, C, d, hd, lo, hi, write_col, int(version == 2), s)
+                     out.data_ptr(), out.stride(0), 1, G, r, C, d, hd, lo, hi, write_col, int(version == 2), None, s)
         return out[:, :M]
 
 
@@ -156,10 +156,11 @@ def _check_batched(zT, wk, q_cat, wq_t, k_new, u):
 
 
 def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=None, k_new=None, write_col: int = -1,
-                  out=None, u_out=None):
+                  out=None, u_out=None, hist=None):
     """Batched parity-mode score: optional z-column write of k_new, u from (q_cat, wq_t) or given, scan of [lo, hi).
 
     zT [B,G,r,C] bf16; q_cat [B,G,hd]; wq_t [G,hd,r]; u [B,G,r] fp32; k_new [B,G,d]. Returns fp32 [B, G, hi-lo].
+    hist: optional zeroed int32 [B, G, 2048] that receives the scores' first-digit histogram for select_rows.
     """
     B, G, r, C, d, hd = _check_batched(zT, wk, q_cat, wq_t, k_new, u)
     lo, hi = int(lo), int(hi)
@@ -175,10 +176,17 @@ def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=Non
         raise ValueError(f"out must be a contiguous float32 [{B}, {G}, >= {M}] tensor")
     if u_out is not None and (u_out.dtype != torch.float32 or tuple(u_out.shape) != (B, G, r) or not u_out.is_contiguous()):
         raise ValueError("u_out must be a contiguous float32 [B, G, r] tensor")
+    check_hist(hist, B, G, zT.device)
     nat.call("attnlab_score_grouped", zT.data_ptr(), nat.ptr(k_new), nat.ptr(wk), nat.ptr(q_cat), nat.ptr(wq_t),
              nat.ptr(u), nat.ptr(u_out), out.data_ptr(), out.shape[2], B, G, r, C, d, hd, lo, hi,
-             write_col if k_new is not None else 0, 1, nat.stream_of(zT.device))
+             write_col if k_new is not None else 0, 1, nat.ptr(hist), nat.stream_of(zT.device))
     return out[..., :M]
+
+
+def check_hist(hist, B, G, device):
+    if hist is not None and (hist.dtype != torch.int32 or tuple(hist.shape) != (B, G, nat.HIST_BINS)
+                             or not hist.is_contiguous() or hist.device != device):
+        raise ValueError(f"hist must be a contiguous int32 [{B}, {G}, {nat.HIST_BINS}] tensor on the scores' device")
 
 
 def project_queries(q_pre, wq_t_scaled):

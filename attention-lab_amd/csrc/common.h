@@ -31,6 +31,8 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 __device__ __forceinline__ float f16_to_f32(uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // a.lo*b.lo + a.hi*b.hi + c on packed bf16 pairs (v_dot2_f32_bf16), fp32 accumulate.
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {

@@ -1,7 +1,9 @@
-// One layer's sparse decode read as a single C-ABI call: score (z column + u + candidate scan) -> select (top-k + F
-// merge) -> gather-free attend, three launches on the caller's stream with the intermediate scores and row list in a
-// caller-provided workspace. Counterpart of sparse_decode_step_kernel (decode.py:145-163).
+// One layer's sparse decode read as a single C-ABI call: score (z column + u + candidate scan + first-digit
+// histogram) -> select (top-k + F merge) -> gather-free attend (+ split-K merge), launched in order on the caller's
+// stream with the intermediate scores, histograms and row list in a caller-provided workspace. Counterpart of
+// sparse_decode_step_kernel (decode.py:145-163).
 #include "common.h"
+#include "select.h"
 
 namespace {
 
@@ -10,11 +12,14 @@ constexpr int64_t kAlign = 256;
 inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-    int64_t scores, rows, part, total;
+    int64_t scores, rows, u, part, total;
     int64_t score_stride;
 };
 
-// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | partials [BG, P, h, 130] fp32.
+// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | partials
+// [BG, P, h, 130] fp32. The
+// top-k histograms live in their own buffer: a region inside this shape-dependent layout would overlap other data
+// of a differently shaped earlier call and not be zero.
 Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     Layout L{};
     const int64_t BG = (int64_t)B * G;
@@ -23,7 +28,8 @@ Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     L.score_stride = (M + 3) / 4 * 4;
     L.scores = 0;
     L.rows = align_up(k > 0 ? BG * L.score_stride * 4 : 0);
-    L.part = L.rows + align_up(BG * S * 4);
+    L.u = L.rows + align_up(BG * S * 4);
+    L.part = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
     L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
     return L;
 }
@@ -39,7 +45,9 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
                                           const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
                                           const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
                                           int legal, int k, int write_col, float scale, int order, int P,
-                                          void* workspace, int64_t workspace_bytes, int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+                                          uint32_t* hist, void* workspace, int64_t workspace_bytes,
+                                          int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+    using namespace attnlab;
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
                     lo, hi, legal, C);
@@ -49,7 +57,9 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     ATTNLAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, "workspace of %lld bytes needed, got %lld",
                     (long long)L.total, (long long)workspace_bytes);
     ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, "workspace must be 256-byte aligned");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
+    if (k == 0) hist = nullptr;
     float* scores = reinterpret_cast<float*>(ws + L.scores);
     int32_t* rows = rows_out ? rows_out : reinterpret_cast<int32_t*>(ws + L.rows);
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
@@ -57,17 +67,19 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     const int d = 128;
     int rc;
     if (k > 0) {
-        rc = attnlab_score_grouped(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, scores, L.score_stride, B, G, r, C, d,
-                                   h * d, lo, hi, write_col, 1, stream);
+        // u_out in the workspace selects the two-launch score: u and the z column once per (b, g), then the scan
+        rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, reinterpret_cast<float*>(ws + L.u), scores,
+                                L.score_stride, B, G, r, C, d,
+                                h * d, lo, hi, write_col, 1, hist, s);
     } else if (k_new) {
         // no candidate is read this step, but the newest key still gets its index column (empty scan range)
-        rc = attnlab_score_grouped(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, nullptr, 0, B, G, r, C, d, h * d, lo, lo,
-                                   write_col, 1, stream);
+        rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, nullptr, 0, B, G, r, C, d, h * d, lo, lo,
+                                write_col, 1, nullptr, s);
     } else {
         rc = ATTNLAB_OK;
     }
     if (rc) return rc;
-    rc = attnlab_select_rows(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, stream);
+    rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, hist, s);
     if (rc) return rc;
     return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
 }

@@ -1,0 +1,33 @@
+// Pieces shared by the score and select kernels: the order-preserving score key and the first radix digit, whose
+// per-row histogram the score kernel builds for the select kernel in the fused decode step.
+#pragma once
+
+#include "common.h"
+
+namespace attnlab {
+
+constexpr int kHistBits = 11;                 // first digit: sign, exponent and the top two mantissa bits
+constexpr int kHistBins = 1 << kHistBits;
+constexpr int kHistShift = 32 - kHistBits;
+
+// Order-preserving key: larger float -> larger key; -0 -> +0; NaN -> 0 (below -inf, whose key is 0x007fffff).
+__device__ __forceinline__ uint32_t score_key(float f) {
+    if (f != f) return 0u;
+    uint32_t u = __float_as_uint(f);
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// attnlab_select_rows with an optional first-digit histogram [B*G][kHistBins] (zero before the score kernel adds to
+// it; left zeroed by the select kernel).
+int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
+                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* hist,
+                     hipStream_t stream);
+
+// attnlab_score_grouped with an optional first-digit histogram output (see select_rows_impl).
+int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                       const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride, int B,
+                       int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector, uint32_t* hist,
+                       hipStream_t stream);
+
+}  // namespace attnlab

@@ -1,0 +1,411 @@
+#!/usr/bin/env python3
+"""Benchmark of the sparse-decode hot path on one MI355X.
+
+Workload (its attention geometry): a Qwen3-8B-shaped stack of 36 layers, each with its own
+bf16 K/V cache [16, 8, 32768, 128] and bf16 index table [16, 8, 32, 32768] resident in HBM (~87 GB), 4 query heads
+per KV group, one r=32 grouped indexer per layer (seeded as the reference seeds them), rho = 1/32 -> k = 1024 of the
+32700 candidates, S = 1092 rows per (b, g). Synthetic data: K, V, index keys, queries ~ N(0, 1).
+
+One step = one decode step of the attention hot path over all 36 layers for the whole batch: per layer, z column
+write + u projection + candidate scan, top-k + merge with F, gather-free split-K attention (the D read), captured in a
+HIP graph and replayed. `value` = batch x steps / elapsed = tokens/s of that path; the same step with the dense decode
+kernel (the A read) is timed beside it. Per-kernel averages come from HIP events around graphs of one kernel type.
+
+The CPU baseline runs the reference's own op sequence (matmul, torch.topk, cat, index_select, SDPA; oracle/ref_path)
+on the host cores for a bounded sample of layer-steps of the same shapes, and is reported, not targeted.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "attention-lab_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0
+DEFAULT_METRIC = "decode tok/s @32K ctx ρ=1/32; per-layer score+topk+attend µs; HBM GB/s %peak"
+
+
+def metric_name() -> str:
+    try:
+        with open(os.path.join(ROOT, "BASELINE.json"), encoding="utf-8") as f:
+            return json.load(f)["metric"]
+    except (OSError, KeyError, ValueError):
+        return DEFAULT_METRIC
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--groups", type=int, default=8)
+    ap.add_argument("--heads-per-group", type=int, default=4)
+    ap.add_argument("--index-dim", type=int, default=32)
+    ap.add_argument("--rho", type=float, default=1 / 32)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 per-layer figures")
+    ap.add_argument("--kernel-reps", type=int, default=20, help="graph replays per kernel-average measurement")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# workload
+# ---------------------------------------------------------------------------------------------------------------------
+class LayerStack:
+    """Per-layer caches, index tables, weights and queries of one decode step, plus preallocated outputs."""
+
+    def __init__(self, torch, dev, *, batch, groups, hpg, context, layers, r, rho, seed):
+        from attention_lab.decode import prepare_request
+        from attention_lab.indexer import GroupedIndexer
+        self.B, self.G, self.h, self.d, self.r, self.L, self.n = batch, groups, hpg, 128, r, context, layers
+        self.C = context
+        B, G, h, d, C = self.B, self.G, self.h, self.d, self.C
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        bf = torch.bfloat16
+        self.K, self.V, self.zT, self.q, self.q_cat, self.k_new, self.wq_t, self.wk = ([] for _ in range(8))
+        for l in range(layers):
+            self.K.append(torch.randn(B, G, C, d, device=dev, dtype=bf, generator=gen))
+            self.V.append(torch.randn(B, G, C, d, device=dev, dtype=bf, generator=gen))
+            self.zT.append(torch.randn(B, G, r, C, device=dev, dtype=bf, generator=gen))
+            self.q.append(torch.randn(B, G, h, d, device=dev, dtype=bf, generator=gen))
+            self.q_cat.append(torch.randn(B, G, h * d, device=dev, dtype=bf, generator=gen))
+            self.k_new.append(torch.randn(B, G, d, device=dev, dtype=bf, generator=gen))
+            idx = GroupedIndexer(G, h, d, r, device=dev, dtype=bf, seed=seed * 1000 + l)
+            self.wq_t.append(idx.wq_t_scaled)
+            self.wk.append(idx.wk)
+        req = prepare_request(B, G, C, valid_length=context, query_position=context - 1, rho=rho, device=dev)
+        self.req = req
+        self.lo, self.hi, self.k = req.layout.candidate_lo, req.layout.candidate_hi, req.k
+        self.S, self.write_col, self.k0 = req.selected_count, req.write_col, req.k0
+        self.M = self.hi - self.lo
+        self.out = [torch.empty(B, G, h, d, device=dev, dtype=bf) for _ in range(layers)]
+        self.dense_out = [torch.empty(B, G, h, d, device=dev, dtype=bf) for _ in range(layers)]
+        self.scores = torch.empty(B, G, (self.M + 3) // 4 * 4, device=dev, dtype=torch.float32)
+        self.rows = torch.empty(B, G, self.S, device=dev, dtype=torch.int32)
+
+    # -- algorithmic bytes per launch (per layer) --
+    def scan_bytes(self):
+        """The scan kernel: index-table columns [lo, hi) read, fp32 scores written (u is 128 B per (b, g))."""
+        return self.B * self.G * (self.r * self.M * 2 + 4 * self.M)
+
+    def score_bytes(self):
+        B, G, h, d, r, M = self.B, self.G, self.h, self.d, self.r, self.M
+        return B * G * (r * M * 2 + 4 * M + r * 2 + (h * d + d) * 2) + G * (h * d * r + r * d) * 2
+
+    def select_bytes(self):
+        return self.B * self.G * (4 * self.M + 4 * self.k)
+
+    def attend_bytes(self):
+        B, G, h, d, S = self.B, self.G, self.h, self.d, self.S
+        return B * G * (S * d * 2 * 2 + 4 * S + h * d * 2 + h * d * 2)
+
+    def dense_bytes(self):
+        B, G, h, d = self.B, self.G, self.h, self.d
+        return B * G * (self.L * d * 2 * 2 + h * d * 2 * 2)
+
+
+def launchers(ls, torch):
+    """Callables that launch one layer's work on the current stream (no allocation, no sync)."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_attend
+    lib = nat.lib()
+    dev = ls.K[0].device
+    B, G, h, d, r, C = ls.B, ls.G, ls.h, ls.d, ls.r, ls.C
+    P = hip_attend.auto_partitions(B * G, ls.S, max_p=hip_attend.MAX_P, min_rows=64)
+    Pd = hip_attend.auto_partitions(B * G, ls.L, max_p=hip_attend.MAX_P_DENSE, min_rows=256)
+    ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    part = torch.empty(B * G * max(P, Pd) * h * 130, dtype=torch.float32, device=dev)
+    # top-k histograms: zero once; each score/select pair leaves them zeroed
+    step_hist = torch.zeros(B * G * nat.HIST_BINS, dtype=torch.int32, device=dev)
+    hist = torch.zeros(B * G * nat.HIST_BINS, dtype=torch.int32, device=dev)
+    u_buf = torch.zeros(B * G * r, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(d)
+
+    def stream():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def sparse(l):
+        nat.call("attnlab_sparse_decode_step", ls.q[l].data_ptr(), ls.q_cat[l].data_ptr(), ls.K[l].data_ptr(),
+                 ls.V[l].data_ptr(), ls.zT[l].data_ptr(), ls.wq_t[l].data_ptr(), ls.wk[l].data_ptr(),
+                 ls.k_new[l].data_ptr(), B, G, h, r, C, ls.lo, ls.hi, ls.L, ls.k, ls.write_col, scale,
+                 nat.ORDER_POSITION, P, step_hist.data_ptr(), ws.data_ptr(), ws_bytes, None, None,
+                 ls.out[l].data_ptr(), stream())
+
+    def dense(l):
+        nat.call("attnlab_dense_decode", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(), B, G,
+                 h, ls.L, C, Pd, scale, ls.dense_out[l].data_ptr(), 1, part.data_ptr(), stream())
+
+    def score(l):   # u/z prologue + scan, as in the fused step
+        nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
+                 ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), None, u_buf.data_ptr(), ls.scores.data_ptr(),
+                 ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1, hist.data_ptr(), stream())
+
+    def scan(l):    # the scan kernel alone (u given): the dominant kernel of the step
+        nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), None, None, None, None, u_buf.data_ptr(), None,
+                 ls.scores.data_ptr(), ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1,
+                 hist.data_ptr(), stream())
+
+    def select(l):
+        nat.call("attnlab_select_rows", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
+                 nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), stream())
+
+    def score_select(l):
+        score(l)
+        select(l)
+
+    def attend(l):
+        nat.call("attnlab_attend", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(),
+                 ls.rows.data_ptr(), ls.S, B, G, h, ls.S, C, P, scale, ls.out[l].data_ptr(), 1, part.data_ptr(),
+                 stream())
+
+    return {"sparse": sparse, "dense": dense, "score": score, "scan": scan, "select": select, "attend": attend,
+            "score_select": score_select, "hist": hist, "partitions": P, "dense_partitions": Pd,
+            "_keep": (ws, part, step_hist, u_buf)}
+
+
+def kernel_breakdown(torch, fns, ls, reps):
+    """Average us per layer of each stage of the fused step, from graphs of 36 launches on consistent data: the
+    scan kernel alone, score (u/z prologue + scan), score + select (the select consumes and clears the histogram the
+    scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend (+ split-K merge)."""
+    t_scan = time_graph(torch, capture(torch, fns["scan"], ls.n), reps, 3) / ls.n
+    t_score = time_graph(torch, capture(torch, fns["score"], ls.n), reps, 3) / ls.n
+    fns["hist"].zero_()
+    torch.cuda.synchronize()
+    t_pair = time_graph(torch, capture(torch, fns["score_select"], ls.n), reps, 3) / ls.n
+    t_attend = time_graph(torch, capture(torch, fns["attend"], ls.n), reps, 3) / ls.n
+    return {"scan": t_scan * 1e3, "score": t_score * 1e3, "select": (t_pair - t_score) * 1e3,
+            "attend": t_attend * 1e3}
+
+
+def capture(torch, fn, layers):
+    """A HIP graph that runs fn(l) for every layer in order."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for l in range(layers):
+            fn(l)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for l in range(layers):
+            fn(l)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps   # ms per replay
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+# CPU baseline: the reference's op sequence on the host cores
+# ---------------------------------------------------------------------------------------------------------------------
+def cpu_baseline(torch, ls, budget_s, layers_in_step):
+    from oracle import ref_path
+    threads = torch.get_num_threads()
+    B, G, h, d = ls.B, ls.G, ls.h, ls.d
+    K, V, zT = ls.K[0].cpu(), ls.V[0].cpu(), ls.zT[0].cpu()
+    q = ls.q[0].cpu().view(B, G, h, 1, d)
+    q_pre = ls.q_cat[0].cpu().view(B, G, h, 1, d)
+    k_new = ls.k_new[0].cpu().view(B, G, 1, d)
+    wq_t, wk = ls.wq_t[0].cpu(), ls.wk[0].cpu()
+    with torch.inference_mode():
+        ref_path.sparse_layer_step(q, q_pre, K, V, zT, wq_t, wk, k_new, ls.L, ls.k0)   # warm-up
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s or n < 3:
+            out_cpu, rows_cpu = ref_path.sparse_layer_step(q, q_pre, K, V, zT, wq_t, wk, k_new, ls.L, ls.k0)
+            n += 1
+        t_layer = (time.perf_counter() - t0) / n
+        nd, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < budget_s / 3 or nd < 2:
+            ref_path.dense_layer_step(q, K, V, ls.L)
+            nd += 1
+        t_dense = (time.perf_counter() - t1) / nd
+    return {
+        "value": ls.B / (layers_in_step * t_layer), "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": (f"{n} layer-steps of layer 0 (B={ls.B}, L={ls.L}, G={ls.G}, h={ls.h}, k={ls.k}) through the "
+                   f"reference's op sequence in bf16 (matmul, torch.topk, cat, index_select, SDPA), scaled to "
+                   f"{layers_in_step} layers"),
+        "us_per_layer": t_layer * 1e6, "dense_us_per_layer": t_dense * 1e6, "dense_layer_steps": nd,
+    }, out_cpu, rows_cpu
+
+
+def numerics_vs_cpu(torch, ls, out_cpu, rows_cpu):
+    """Layer 0 on the GPU against the reference's CPU path on the same inputs (bf16 scores there, fp32 here)."""
+    B, G = ls.B, ls.G
+    gpu_out = ls.out[0].float().cpu().view(B, G, ls.h, ls.d)
+    cpu_out = out_cpu.float().view(B, G, ls.h, ls.d)
+    diff = (gpu_out - cpu_out).abs()
+    off = (torch.arange(B * G) * ls.C).view(B, G, 1)
+    cpu_pos = (rows_cpu.view(B, G, -1) - off)
+    gpu_pos = ls.rows.cpu().long() if ls.rows is not None else None
+    agree = []
+    for b in range(B):
+        for g in range(G):
+            a = set(cpu_pos[b, g].tolist())
+            c = set(gpu_pos[b, g].tolist())
+            agree.append(len(a & c) / len(a))
+    return {"out_max_abs": float(diff.max()), "out_mean_abs": float(diff.mean()),
+            "row_set_agreement_mean": sum(agree) / len(agree), "row_set_agreement_min": min(agree),
+            "note": "the CPU path ranks bf16-rounded scores (torch bf16 matmul), the kernel fp32 scores"}
+
+
+# ---------------------------------------------------------------------------------------------------------------------
+def run_b1(torch, dev, args):
+    """Batch-1 per-layer figures at the reference's headline shape (G=8, h=2) and at h=4, 28 layers rotating."""
+    res = {}
+    for hpg in (2, 4):
+        ls = LayerStack(torch, dev, batch=1, groups=8, hpg=hpg, context=args.context, layers=28, r=args.index_dim,
+                        rho=args.rho, seed=args.seed + 7)
+        fns = launchers(ls, torch)
+        gs = capture(torch, fns["sparse"], ls.n)
+        gd = capture(torch, fns["dense"], ls.n)
+        ms_s = time_graph(torch, gs, max(20, args.steps // 2), 5)
+        ms_d = time_graph(torch, gd, max(20, args.steps // 2), 5)
+        per = kernel_breakdown(torch, fns, ls, args.kernel_reps)
+        sparse_bytes = ls.score_bytes() + ls.select_bytes() + ls.attend_bytes()
+        us = ms_s * 1e3 / ls.n
+        res[f"h{hpg}"] = {"sparse_us_per_layer": us, "dense_us_per_layer": ms_d * 1e3 / ls.n,
+                          "kernel_us": per, "sparse_algorithmic_bytes_per_layer": sparse_bytes,
+                          "sparse_gbs": sparse_bytes / (us * 1e-6) / 1e9,
+                          "sparse_frac_of_peak": sparse_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
+        del ls, fns, gs, gd
+        torch.cuda.empty_cache()
+    return res
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one GPU, and the "
+                                   "multi-GPU design (tensor parallel by KV group) is described in DESIGN.md, not run",
+                          "n_gpus": args.gpus}))
+        return 2
+    import torch
+    from attention_lab import _native
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device"}))
+        return 1
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    t_setup = time.perf_counter()
+    ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,
+                    layers=args.layers, r=args.index_dim, rho=args.rho, seed=args.seed)
+    fns = launchers(ls, torch)
+    g_sparse = capture(torch, fns["sparse"], ls.n)
+    g_dense = capture(torch, fns["dense"], ls.n)
+    print(f"[bench] setup {time.perf_counter() - t_setup:.1f}s: {ls.n} layers, B={ls.B}, L={ls.L}, k={ls.k}, "
+          f"S={ls.S}, P={fns['partitions']}, dense P={fns['dense_partitions']}", file=sys.stderr, flush=True)
+
+    # ---- the timed region: exactly `steps` sparse decode steps ----
+    for _ in range(args.warmup):
+        g_sparse.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g_sparse.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    value = ls.B * args.steps / (ms_step * args.steps / 1e3)
+    print(f"[bench] sparse step {ms_step:.3f} ms ({wall:.2f}s wall for {args.steps} steps)", file=sys.stderr, flush=True)
+
+    ms_dense = time_graph(torch, g_dense, max(10, args.steps // 4), 3)
+    kus = kernel_breakdown(torch, fns, ls, args.kernel_reps)
+    print(f"[bench] dense step {ms_dense:.3f} ms; per-kernel us {({k: round(v, 2) for k, v in kus.items()})}",
+          file=sys.stderr, flush=True)
+
+    sb, selb, ab, db = ls.score_bytes(), ls.select_bytes(), ls.attend_bytes(), ls.dense_bytes()
+    score_us = kus["score"]
+    scan_b = ls.scan_bytes()
+    ach = scan_b / (kus["scan"] * 1e-6) / 1e9
+    us_layer = ms_step * 1e3 / ls.n
+    sparse_bytes = sb + selb + ab
+    line = {
+        "metric": metric_name(),
+        "value": value,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "sparse decode read (z append + score + top-k + gather-free attend) over a "
+                               "36-layer Qwen3-8B-shaped KV cache, one HIP graph per step",
+                   "batch": ls.B, "context": ls.L, "layers": ls.n, "kv_groups": ls.G, "heads_per_group": ls.h,
+                   "head_dim": ls.d, "index_dim": ls.r, "rho": args.rho, "k": ls.k, "selected_rows": ls.S,
+                   "global_batch": ls.B, "seq_len": ls.L, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "score_scan_vec (candidate scan of the index table)", "achieved": ach,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": scan_b, "avg_launch_us": kus["scan"]},
+        "per_layer_us": {"sparse": us_layer, "dense": ms_dense * 1e3 / ls.n, "score_prologue_and_scan": score_us,
+                         "scan": kus["scan"], "select": kus["select"], "attend_with_combine": kus["attend"]},
+        "hot_path_hbm": {"algorithmic_bytes_per_layer": sparse_bytes, "gbs": sparse_bytes / (us_layer * 1e-6) / 1e9,
+                         "frac_of_peak": sparse_bytes / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBS},
+        "kernels": {
+            "select": {"bytes": selb, "gbs": selb / (kus["select"] * 1e-6) / 1e9},
+            "attend": {"bytes": ab, "gbs": ab / (kus["attend"] * 1e-6) / 1e9},
+            "dense": {"bytes": db, "gbs": db / (ms_dense * 1e-3 / ls.n) / 1e9,
+                      "frac": db / (ms_dense * 1e-3 / ls.n) / 1e9 / PEAK_HBM_GBS},
+        },
+        "dense_control": {"tok_s": ls.B / (ms_dense / 1e3), "ms_per_step": ms_dense,
+                          "sparse_speedup": ms_dense / ms_step},
+    }
+
+    if not args.no_b1:
+        try:
+            del g_dense
+            line["batch1"] = run_b1(torch, dev, args)
+        except Exception as e:  # the headline line must still print
+            line["batch1"] = {"error": repr(e)}
+
+    if not args.no_cpu_baseline:
+        # layer 0 through the fused step once more so ls.rows holds its row list for the numerics comparison
+        fns["score"](0)
+        fns["select"](0)
+        fns["attend"](0)
+        torch.cuda.synchronize()
+        cb, out_cpu, rows_cpu = cpu_baseline(torch, ls, args.cpu_seconds, ls.n)
+        line["cpu_baseline"] = cb
+        line["numerics_vs_cpu_reference_path"] = numerics_vs_cpu(torch, ls, out_cpu, rows_cpu)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -46,19 +46,19 @@ def test_invalid_arguments_are_rejected_before_any_launch(native_lib):
         _native.call("attnlab_topk", None, 10, 1, 10, 11, 0, None, None, 11, None)
     with pytest.raises(ValueError, match="write_col"):
         _native.call("attnlab_score_grouped", 16, 16, 16, 16, 16, None, None, 16, 100, 1, 8, 32, 128, 128, 256, 4, 100,
-                     50, 1, None)
+                     50, 1, None, None)
     with pytest.raises(ValueError, match="index width"):
         _native.call("attnlab_score_grouped", 16, None, 16, 16, 16, None, None, 16, 100, 1, 8, 33, 128, 128, 256, 4, 100,
-                     120, 1, None)
+                     120, 1, None, None)
     with pytest.raises(ValueError, match="h=9"):
         _native.call("attnlab_attend", 16, 16, 128 * 128, 128, 16, 16, 10, 1, 8, 9, 10, 128, 1, 0.1, 16, 1, None, None)
     with pytest.raises(ValueError, match="partitions"):
         _native.call("attnlab_dense_decode", 16, 16, 128 * 128, 128, 16, 1, 8, 2, 10, 128, 0, 0.1, 16, 1, None, None)
     with pytest.raises(ValueError, match="legal"):
-        _native.call("attnlab_select_rows", 16, 10, 1, 8, 4, 20, 10, 3, 100, 0, 16, 10, None, None)
+        _native.call("attnlab_select_rows", 16, 10, 1, 8, 4, 20, 10, 3, 100, 0, 16, 10, None, None, None)
     with pytest.raises(ValueError, match="workspace"):
         _native.call("attnlab_sparse_decode_step", *([16] * 8), 1, 8, 2, 32, 4096, 4, 4032, 4096, 128, 4095, 0.1, 0, 4,
-                     256, 10, None, None, 16, None)
+                     None, 256, 10, None, None, 16, None)
 
 
 def test_workspace_size_formula(native_lib):
@@ -66,7 +66,8 @@ def test_workspace_size_formula(native_lib):
         a = lambda x: (x + 255) // 256 * 256  # noqa: E731
         BG, M, S = B * G, hi - lo, lo + (legal - hi) + k
         scores = a(BG * ((M + 3) // 4 * 4) * 4) if k > 0 else 0
-        return scores + a(BG * S * 4) + (a(BG * P * h * 130 * 4) if P > 1 else 0)
+        u = a(BG * 32 * 4) if k > 0 else 0
+        return scores + a(BG * S * 4) + u + (a(BG * P * h * 130 * 4) if P > 1 else 0)
     for args in ((16, 8, 4, 4, 32704, 32768, 1024, 4), (1, 8, 2, 4, 1984, 2048, 64, 1), (2, 8, 2, 60, 60, 60, 0, 8)):
         assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)
     assert native_lib.attnlab_sparse_decode_workspace(0, 8, 2, 4, 100, 164, 3, 1) == -1

@@ -106,6 +106,31 @@ def test_select_rows_matches_oracle(gpu, legal, k0, order):
     assert np.array_equal(flat.cpu().numpy().reshape(B, G, S), want + off)
 
 
+@pytest.mark.parametrize("B,C,L,order", [(1, 2048 + 64, 2048, "position"), (4, 32768, 32768, "score"),
+                                         (2, 70000, 70000, "position"), (3, 1000, 777, "score")])
+def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order):
+    """score_grouped(hist=) + select_rows(hist=) gives exactly the rows of the self-contained select, leaves the
+    histogram zeroed, and stays exact over repeated calls on fresh data (a stale histogram would break it)."""
+    from attention_lab import hip_score
+    from oracle import rules
+    G, r = 8, 32
+    lo, hi, k, S = rules.step(L, rules.budget(L, 1 / 32))
+    hist = torch.zeros(B, G, 2048, dtype=torch.int32, device=gpu)
+    for rep in range(3):
+        gen = torch.Generator().manual_seed(100 * rep + B)
+        zT = torch.randn(B, G, r, C, generator=gen).to(torch.bfloat16).to(gpu)
+        u = torch.randn(B, G, r, generator=gen).to(gpu)
+        s = hip_score.score_grouped(zT, lo, hi, u=u, hist=hist)
+        rows_h, _ = hip_select.select_rows(s, lo, hi, L, k, C, order=order, hist=hist)
+        torch.cuda.synchronize()
+        assert int(hist.abs().sum()) == 0, "the select kernel must leave the histogram zeroed"
+        rows_p, _ = hip_select.select_rows(s, lo, hi, L, k, C, order=order)
+        torch.cuda.synchronize()
+        assert torch.equal(rows_h, rows_p)
+        want = exact.select_rows(s.cpu().numpy(), lo, hi, L, k, order=order)
+        assert np.array_equal(rows_h.cpu().numpy(), want)
+
+
 def test_validation(gpu):
     t = torch.zeros(2, 100, device=gpu)
     with pytest.raises(ValueError):
