@@ -15,8 +15,10 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
-HIST_BINS = 2048   # first radix digit of the top-k: top 11 bits of the order-preserving score key
+ABI_VERSION = 3
+# select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
+# score key), then reserved words, padded to 256 bytes (ATTNLAB_SELECT_STATE_WORDS)
+SELECT_STATE_WORDS = 2112
 
 ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2
 ORDER_POSITION, ORDER_SCORE = 0, 1
@@ -34,7 +36,8 @@ SIGNATURES = {
     "attnlab_project_keys": (_i, [_p, _i64, _i64, _p, _p] + [_i] * 7 + [_p]),
     "attnlab_score_lightning": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 8 + [_p]),
     "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
-    "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p]),
+    "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
+    "attnlab_select_scratch_bytes": (_i64, [_i, _i]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
@@ -106,11 +109,11 @@ def ptr(t) -> int | None:
 
 
 class Workspace:
-    """Growable device scratch owned by one op object (split-K partials, intermediate scores, row lists, top-k
-    histograms).
+    """Growable device scratch owned by one op object (split-K partials, intermediate scores, row lists, select
+    state).
 
-    Buffers are zero-filled when allocated: the top-k histograms must start at zero, and the kernels leave them
-    zeroed after every call. Two launches that share one Workspace must be ordered on one stream. Grow it (one eager
+    Buffers are zero-filled when allocated: the select state (top-k histograms and counters) must start at zero, and
+    the kernels leave it zeroed after every call. Two launches that share one Workspace must be ordered on one stream. Grow it (one eager
     call) before capturing the launches in a HIP graph, so no allocation happens under capture.
     """
 

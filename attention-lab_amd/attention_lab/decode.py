@@ -201,12 +201,13 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     order = nat.ORDER_POSITION if canonical_order else nat.ORDER_SCORE
     nbytes = nat.lib().attnlab_sparse_decode_workspace(B, G, h, lo, hi, legal, k, P)
     ws = _STEP_WS.bytes(k_cache.device, nbytes, "step")
-    hist = _STEP_WS.bytes(k_cache.device, B * G * nat.HIST_BINS * 4, "hist")   # zeroed once, left zeroed by each call
+    # select state: zeroed once, left zeroed by each call
+    state = _STEP_WS.bytes(k_cache.device, B * G * nat.SELECT_STATE_WORDS * 4, "state")
     out = torch.empty(B, G, h, d, dtype=torch.bfloat16, device=k_cache.device)
     flat = torch.empty(B * G * S, dtype=torch.int64, device=k_cache.device) if return_rows else None
     nat.call("attnlab_sparse_decode_step", q.data_ptr(), q_cat.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
              zT.data_ptr(), wq_t_scaled.contiguous().data_ptr(), wk.contiguous().data_ptr(), nat.ptr(k_new), B, G, h, r,
-             C, lo, hi, legal, k, wc, sc, order, P, hist.data_ptr(), ws.data_ptr(), ws.numel(), None, nat.ptr(flat),
+             C, lo, hi, legal, k, wc, sc, order, P, state.data_ptr(), ws.data_ptr(), ws.numel(), None, nat.ptr(flat),
              out.data_ptr(), nat.stream_of(k_cache.device))
     out = out.view(B, G, h, 1, d)
     return (out, flat) if return_rows else out

@@ -156,11 +156,12 @@ def _check_batched(zT, wk, q_cat, wq_t, k_new, u):
 
 
 def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=None, k_new=None, write_col: int = -1,
-                  out=None, u_out=None, hist=None):
+                  out=None, u_out=None, state=None):
     """Batched parity-mode score: optional z-column write of k_new, u from (q_cat, wq_t) or given, scan of [lo, hi).
 
     zT [B,G,r,C] bf16; q_cat [B,G,hd]; wq_t [G,hd,r]; u [B,G,r] fp32; k_new [B,G,d]. Returns fp32 [B, G, hi-lo].
-    hist: optional zeroed int32 [B, G, 2048] that receives the scores' first-digit histogram for select_rows.
+    state: optional zeroed int32 select state [B, G, SELECT_STATE_WORDS] that receives the scores' first-digit
+    histogram for select_rows.
     """
     B, G, r, C, d, hd = _check_batched(zT, wk, q_cat, wq_t, k_new, u)
     lo, hi = int(lo), int(hi)
@@ -176,17 +177,18 @@ def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=Non
         raise ValueError(f"out must be a contiguous float32 [{B}, {G}, >= {M}] tensor")
     if u_out is not None and (u_out.dtype != torch.float32 or tuple(u_out.shape) != (B, G, r) or not u_out.is_contiguous()):
         raise ValueError("u_out must be a contiguous float32 [B, G, r] tensor")
-    check_hist(hist, B, G, zT.device)
+    check_state(state, B, G, zT.device)
     nat.call("attnlab_score_grouped", zT.data_ptr(), nat.ptr(k_new), nat.ptr(wk), nat.ptr(q_cat), nat.ptr(wq_t),
              nat.ptr(u), nat.ptr(u_out), out.data_ptr(), out.shape[2], B, G, r, C, d, hd, lo, hi,
-             write_col if k_new is not None else 0, 1, nat.ptr(hist), nat.stream_of(zT.device))
+             write_col if k_new is not None else 0, 1, nat.ptr(state), nat.stream_of(zT.device))
     return out[..., :M]
 
 
-def check_hist(hist, B, G, device):
-    if hist is not None and (hist.dtype != torch.int32 or tuple(hist.shape) != (B, G, nat.HIST_BINS)
-                             or not hist.is_contiguous() or hist.device != device):
-        raise ValueError(f"hist must be a contiguous int32 [{B}, {G}, {nat.HIST_BINS}] tensor on the scores' device")
+def check_state(state, B, G, device):
+    W = nat.SELECT_STATE_WORDS
+    if state is not None and (state.dtype != torch.int32 or tuple(state.shape) != (B, G, W)
+                              or not state.is_contiguous() or state.device != device):
+        raise ValueError(f"state must be a contiguous int32 [{B}, {G}, {W}] tensor on the scores' device")
 
 
 def project_queries(q_pre, wq_t_scaled):

@@ -52,13 +52,15 @@ def topk(scores, k: int, *, order: str = "score"):
 
 
 def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, order: str = "position",
-                rows=None, want_flat: bool = False, hist=None):
+                rows=None, want_flat: bool = False, state=None, tiled: bool = True):
     """Row list of one decode step from candidate scores [B, G, hi-lo] (fp32, unit column stride).
 
     Returns (rows int32 [B, G, S] original positions, flat int64 [B*G*S] row ids of the flattened cache or None),
     S = lo + (legal - hi) + k. order="position" sorts every list ascending (canonical_order); order="score" puts F
     first and then the candidates by descending score, like cat(fixed_rows, topk.indices) in decode.py:93.
-    hist: the first-digit histograms score_grouped(..., hist=) built for these scores (cleared here), or None.
+    state: the select state score_grouped(..., state=) filled for these scores (cleared here), or None. With a state,
+    position order and tiled=True the keys are classified by a grid of 4096-key tiles and each row resolved by one
+    workgroup (same result as the single-workgroup select).
     """
     if scores.dim() != 3 or scores.dtype != torch.float32 or not scores.is_cuda or scores.stride(2) != 1:
         raise ValueError("scores must be a float32 [B, G, M] tensor with unit column stride on a HIP device")
@@ -81,11 +83,17 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
     if stride is None:
         scores = scores.contiguous()
         stride = max(M, 1)
-    if hist is not None and (hist.dtype != torch.int32 or tuple(hist.shape) != (B, G, nat.HIST_BINS)
-                             or not hist.is_contiguous() or hist.device != scores.device):
-        raise ValueError(f"hist must be a contiguous int32 [{B}, {G}, {nat.HIST_BINS}] tensor on the scores' device")
+    W = nat.SELECT_STATE_WORDS
+    if state is not None and (state.dtype != torch.int32 or tuple(state.shape) != (B, G, W)
+                              or not state.is_contiguous() or state.device != scores.device):
+        raise ValueError(f"state must be a contiguous int32 [{B}, {G}, {W}] tensor on the scores' device")
+    scratch = None
+    if state is not None and tiled and code == nat.ORDER_POSITION and k > 0:
+        nbytes = nat.lib().attnlab_select_scratch_bytes(B * G, M)
+        scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=scores.device)
     nat.call("attnlab_select_rows", scores.data_ptr(), stride, B, G, lo, hi, legal, k, capacity, code,
-             rows.data_ptr(), S, nat.ptr(flat), nat.ptr(hist), nat.stream_of(scores.device))
+             rows.data_ptr(), S, nat.ptr(flat), nat.ptr(state), nat.ptr(scratch),
+             0 if scratch is None else scratch.numel(), nat.stream_of(scores.device))
     return rows, flat
 
 

@@ -56,6 +56,31 @@ __device__ __forceinline__ float sum8(float x) {
     return x;
 }
 
+// x shifted across lanes by DPP control CTRL; lanes whose source is outside the row (or whose row is masked off by
+// ROW_MASK) read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32_or_zero(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xf, true);
+}
+
+// Inclusive prefix sum within each row of 16 lanes (row_shr 1, 2, 4, 8).
+__device__ __forceinline__ uint32_t row16_incl_scan(uint32_t x) {
+    x += dpp_u32_or_zero<0x111, 0xf>(x);
+    x += dpp_u32_or_zero<0x112, 0xf>(x);
+    x += dpp_u32_or_zero<0x114, 0xf>(x);
+    x += dpp_u32_or_zero<0x118, 0xf>(x);
+    return x;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: the row scans, then row_bcast:15 carries row 0's (row 2's) total
+// into row 1 (row 3), and row_bcast:31 carries the lower half's total into rows 2 and 3. Six DPP adds, no LDS.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+    x = row16_incl_scan(x);
+    x += dpp_u32_or_zero<0x142, 0xa>(x);
+    x += dpp_u32_or_zero<0x143, 0xc>(x);
+    return x;
+}
+
 __device__ __forceinline__ float shfl_xor_f32(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
 // exp2 on the hardware transcendental unit (v_exp_f32); exp2(-inf) = 0.

@@ -1,6 +1,6 @@
 // One layer's sparse decode read as a single C-ABI call: score (z column + u + candidate scan + first-digit
 // histogram) -> select (top-k + F merge) -> gather-free attend (+ split-K merge), launched in order on the caller's
-// stream with the intermediate scores, histograms and row list in a caller-provided workspace. Counterpart of
+// stream with the intermediate scores, select scratch and row list in a caller-provided workspace. Counterpart of
 // sparse_decode_step_kernel (decode.py:145-163).
 #include "common.h"
 #include "select.h"
@@ -12,14 +12,14 @@ constexpr int64_t kAlign = 256;
 inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-    int64_t scores, rows, u, part, total;
+    int64_t scores, rows, u, sel, part, total;
     int64_t score_stride;
 };
 
-// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | partials
-// [BG, P, h, 130] fp32. The
-// top-k histograms live in their own buffer: a region inside this shape-dependent layout would overlap other data
-// of a differently shaped earlier call and not be zero.
+// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | tiled-select scratch |
+// partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state (first-digit histograms and
+// candidate counters, which must start at zero) lives in its own buffer: a region inside this shape-dependent layout
+// would overlap other data of a differently shaped earlier call.
 Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     Layout L{};
     const int64_t BG = (int64_t)B * G;
@@ -29,7 +29,8 @@ Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     L.scores = 0;
     L.rows = align_up(k > 0 ? BG * L.score_stride * 4 : 0);
     L.u = L.rows + align_up(BG * S * 4);
-    L.part = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
+    L.sel = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
+    L.part = L.sel + align_up(k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M) : 0);
     L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
     return L;
 }
@@ -45,7 +46,7 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
                                           const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
                                           const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
                                           int legal, int k, int write_col, float scale, int order, int P,
-                                          uint32_t* hist, void* workspace, int64_t workspace_bytes,
+                                          uint32_t* state, void* workspace, int64_t workspace_bytes,
                                           int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
     using namespace attnlab;
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
@@ -59,7 +60,7 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, "workspace must be 256-byte aligned");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
-    if (k == 0) hist = nullptr;
+    if (k == 0) state = nullptr;
     float* scores = reinterpret_cast<float*>(ws + L.scores);
     int32_t* rows = rows_out ? rows_out : reinterpret_cast<int32_t*>(ws + L.rows);
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
@@ -70,7 +71,7 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
         // u_out in the workspace selects the two-launch score: u and the z column once per (b, g), then the scan
         rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, reinterpret_cast<float*>(ws + L.u), scores,
                                 L.score_stride, B, G, r, C, d,
-                                h * d, lo, hi, write_col, 1, hist, s);
+                                h * d, lo, hi, write_col, 1, state, s);
     } else if (k_new) {
         // no candidate is read this step, but the newest key still gets its index column (empty scan range)
         rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, nullptr, 0, B, G, r, C, d, h * d, lo, lo,
@@ -79,7 +80,8 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
         rc = ATTNLAB_OK;
     }
     if (rc) return rc;
-    rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, hist, s);
+    rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
+                          k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
     if (rc) return rc;
     return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
 }

@@ -29,7 +29,7 @@ struct ScoreArgs {
     int64_t out_stride;
     int G, r, C, d, hd, lo, M, write_col;
     int tiles;              // column tiles per (b, g) row
-    uint32_t* hist;         // [BG, kHistBins] first-digit histograms for the select kernel, or null
+    uint32_t* hist;         // [BG, kSelectStateWords] select state: first-digit histogram bins first, or null
 };
 
 constexpr int kMaxR = 32;
@@ -108,7 +108,7 @@ __device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
 template <int BLOCK>
 __device__ __forceinline__ void flush_histogram(uint32_t* hsh, uint32_t* ghist, int bg) {
     __syncthreads();
-    uint32_t* row = ghist + (size_t)bg * kHistBins;
+    uint32_t* row = ghist + (size_t)bg * kSelectStateWords;
     for (int b = threadIdx.x; b < kHistBins; b += BLOCK) {
         const uint32_t c = hsh[b];
         if (c) atomicAdd(row + b, c);

@@ -9,6 +9,9 @@ namespace attnlab {
 constexpr int kHistBits = 11;                 // first digit: sign, exponent and the top two mantissa bits
 constexpr int kHistBins = 1 << kHistBits;
 constexpr int kHistShift = 32 - kHistBits;
+// Per-row select state shared by the score and select kernels: the first-digit histogram (kHistBins words), then
+// reserved words, padded to 256 bytes. Zero before the first call; the select leaves it zero.
+constexpr int kSelectStateWords = 2112;
 
 // Order-preserving key: larger float -> larger key; -0 -> +0; NaN -> 0 (below -inf, whose key is 0x007fffff).
 __device__ __forceinline__ uint32_t score_key(float f) {
@@ -18,13 +21,16 @@ __device__ __forceinline__ uint32_t score_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// attnlab_select_rows with an optional first-digit histogram [B*G][kHistBins] (zero before the score kernel adds to
-// it; left zeroed by the select kernel).
+// attnlab_select_rows: `state` [B*G][kSelectStateWords] (nullable) holds the first-digit histograms the score kernel
+// built; with it and a scratch of select_scratch_bytes(B*G, M) the position-order select runs tiled over the chip.
 int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
-                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* hist,
-                     hipStream_t stream);
+                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                     void* scratch, int64_t scratch_bytes, hipStream_t stream);
 
-// attnlab_score_grouped with an optional first-digit histogram output (see select_rows_impl).
+// Scratch bytes of the tiled select for R rows of M candidates (no zeroing needed).
+int64_t select_scratch_bytes(int R, int M);
+
+// attnlab_score_grouped with an optional select-state output: per row, the first-digit histogram of the scores.
 int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                        const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride, int B,
                        int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector, uint32_t* hist,

@@ -36,7 +36,8 @@ struct SelectArgs {
     int32_t* top_idx;
     float* top_val;
     int64_t top_stride;
-    // first-digit histograms [R][kHistBins] built by the score kernel (nullable); cleared here after use
+    // select state [R][kSelectStateWords] whose first kHistBins words are the first-digit histogram built by the score
+    // kernel (nullable); cleared here after use
     uint32_t* hist;
 };
 
@@ -47,42 +48,46 @@ struct SelectShared {
     uint64_t sortbuf[kMaxScoreOrderK];
 };
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    return x;
-}
-
-// Block-wide exclusive scan of two counters at once (1024 threads). Ends with the block synchronised.
-__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_t& ea, uint32_t& eb, SelectShared& sh) {
+// Block-wide exclusive scan of two counters for THREADS (<= 1024) threads; tot_a / tot_b receive the block totals.
+// The wave totals are scanned by every wave at once: lanes 0..15 hold the first counter's, lanes 16..31 the second's,
+// and one row-local DPP scan covers both. Ends synchronised.
+template <int THREADS>
+__device__ __forceinline__ void block_scan2(uint32_t a, uint32_t b, uint32_t& ea, uint32_t& eb, uint32_t& tot_a,
+                                            uint32_t& tot_b, uint32_t (*wave_tot)[2]) {
+    constexpr int kWaves = THREADS / 64;
+    static_assert(kWaves <= 16, "one row of 16 lanes per counter");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t ia = wave_incl_scan(a, lane), ib = wave_incl_scan(b, lane);
+    const uint32_t ia = wave_incl_scan(a), ib = wave_incl_scan(b);
     if (lane == 63) {
-        sh.wave_tot[wave][0] = ia;
-        sh.wave_tot[wave][1] = ib;
+        wave_tot[wave][0] = ia;
+        wave_tot[wave][1] = ib;
     }
     __syncthreads();
-    uint32_t oa = 0, ob = 0;
-    for (int w = 0; w < wave; ++w) {
-        oa += sh.wave_tot[w][0];
-        ob += sh.wave_tot[w][1];
-    }
-    ea = oa + ia - a;
-    eb = ob + ib - b;
+    uint32_t v = 0;
+    if (lane < kWaves) v = wave_tot[lane][0];
+    else if (lane >= 16 && lane < 16 + kWaves) v = wave_tot[lane - 16][1];
+    const uint32_t vi = row16_incl_scan(v);
+    const uint32_t ve = vi - v;
+    ea = (uint32_t)__builtin_amdgcn_readlane((int)ve, wave) + ia - a;
+    eb = (uint32_t)__builtin_amdgcn_readlane((int)ve, 16 + wave) + ib - b;
+    tot_a = (uint32_t)__builtin_amdgcn_readlane((int)vi, 15);
+    tot_b = (uint32_t)__builtin_amdgcn_readlane((int)vi, 31);
     __syncthreads();
 }
 
-// With the histogram of one digit complete in sh.hist[0..nbins), find the digit D holding the krem-th largest key:
+__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_t& ea, uint32_t& eb, SelectShared& sh) {
+    uint32_t ta, tb;
+    block_scan2<kSelThreads>(a, b, ea, eb, ta, tb, sh.wave_tot);
+}
+
+// With the histogram of one digit complete in hist[0..nbins) (LDS), find the digit D holding the krem-th largest key:
 // count(digit > D) < krem <= count(digit >= D). Thread t owns bins [2t, 2t+1]; the counts above a thread come from
 // an exclusive scan over the threads in reverse order. Publishes D and the new krem; ends synchronised.
-__device__ __forceinline__ void find_digit(SelectShared& sh, uint32_t krem, int nbins) {
+__device__ __forceinline__ void find_digit(SelectShared& sh, const uint32_t* hist, uint32_t krem, int nbins) {
     const int tid = threadIdx.x;
     const int rt = kSelThreads - 1 - tid;       // reverse rank: thread 1023 owns the lowest bins
     const int b0 = 2 * rt;
-    const uint32_t c0 = b0 < nbins ? sh.hist[b0] : 0u, c1 = b0 + 1 < nbins ? sh.hist[b0 + 1] : 0u;
+    const uint32_t c0 = b0 < nbins ? hist[b0] : 0u, c1 = b0 + 1 < nbins ? hist[b0 + 1] : 0u;
     uint32_t above, unused;
     block_excl_scan2(c0 + c1, 0u, above, unused, sh);   // keys in bins owned by lower tids = higher bins
     if (above < krem && above + c1 >= krem) {
@@ -123,7 +128,7 @@ __device__ __forceinline__ uint32_t radix_threshold(int k, int M, ForEach for_ea
             });
             __syncthreads();
         }
-        find_digit(sh, krem, nb);
+        find_digit(sh, sh.hist, krem, nb);
         prefix |= sh.digit << shift;
         pmask |= dmask << shift;
         krem = sh.krem;
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
     const int M = a.M;
     const int seg = tid * KPT;
     const int nvalid = max(0, min(KPT, M - seg));
-    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kHistBins : nullptr;
+    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kSelectStateWords : nullptr;
     uint32_t key[KPT];
     const bool vec = ((reinterpret_cast<uintptr_t>(s) & 15) == 0) && (KPT % 4 == 0);
     if (vec && nvalid == KPT) {
@@ -303,15 +308,15 @@ __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
     finish_row(a, row, sh);
 }
 
-// Long rows: keys are re-read from global memory in every pass.
-__global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a, int seglen) {
-    __shared__ SelectShared sh;
-    const int row = blockIdx.x;
+// One row with 1024 threads, keys re-read from global memory in every pass (any M). Used for long rows and as the
+// fallback of the tiled select.
+__device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared& sh) {
     const int tid = threadIdx.x;
+    const int seglen = (a.M + kSelThreads - 1) / kSelThreads;
     const float* s = a.scores + (size_t)row * a.score_stride;
     const int seg = tid * seglen;
     const int nvalid = max(0, min(seglen, a.M - seg));
-    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kHistBins : nullptr;
+    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kSelectStateWords : nullptr;
     if (a.k > 0) {
         uint32_t krem = 0;
         const uint32_t T = radix_threshold(a.k, a.M, [&](auto fn) {
@@ -345,6 +350,11 @@ __global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a, int s
     finish_row(a, row, sh);
 }
 
+__global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a) {
+    __shared__ SelectShared sh;
+    select_row_streaming(a, blockIdx.x, sh);
+}
+
 static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
     const int kpt = (a.M + kSelThreads - 1) / kSelThreads;
     const dim3 grid(R), block(kSelThreads);
@@ -352,13 +362,259 @@ static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
     else if (kpt <= 8) hipLaunchKernelGGL(select_reg<8>, grid, block, 0, s, a);
     else if (kpt <= 16) hipLaunchKernelGGL(select_reg<16>, grid, block, 0, s, a);
     else if (kpt <= 32) hipLaunchKernelGGL(select_reg<32>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(select_stream, grid, block, 0, s, a, kpt);
+    else hipLaunchKernelGGL(select_stream, grid, block, 0, s, a);
     return check_launch("select");
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Tiled select (position order, first-digit histogram given), two launches:
+//   A select_classify  (rows x tiles of 4096 keys, 256 threads): the threshold's first digit b1 from the row
+//                      histogram; every key of the tile is classified as "above" (first digit > b1: selected for sure)
+//                      or "candidate" (first digit == b1), written as two bitmaps of the row (one bit per key).
+//   B select_resolve   (one 1024-thread workgroup per row): compacts the candidate bitmap into an index-ordered list,
+//                      gathers the candidates' scores, finds the threshold among them with the remaining two radix
+//                      digits, takes the tied keys at the threshold in index order, ORs the selected candidates into
+//                      the "above" bitmap in LDS and writes the set bits in index order (plus F); it then clears the
+//                      row's histogram. A row with more than kCandCap candidates runs the single-workgroup select.
+// Every kernel issues its global loads before it uses any of them: each is a few memory round trips long.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kTileKeys = 4096;
+constexpr int kTileThreads = 256;
+constexpr int kTileKPT = kTileKeys / kTileThreads;   // 16 keys per thread, one contiguous segment (half a bitmap word)
+constexpr int kCandCap = 4096;                        // candidates per row, listed in LDS
+constexpr int kCandPerThread = kCandCap / kSelThreads;
+constexpr int kMaxWords = 8192;                       // bitmap words per row held in LDS: M <= 262144
+constexpr int kMaxWordsPerThread = kMaxWords / kSelThreads;
+
+struct TiledArgs {
+    uint32_t* above;   // [R, W] bit i: key i's first digit > b1
+    uint32_t* cand;    // [R, W] bit i: key i's first digit == b1
+    int W;             // bitmap words per row = ceil(M / 32)
+    int T;             // tiles per row
+};
+
+__host__ __device__ inline int64_t tiled_scratch_bytes(int R, int M) {
+    return (int64_t)R * 2 * 4 * (((int64_t)M + 31) / 32);
+}
+
+// b1 = first digit of the k-th largest key, from the row histogram; thread t holds the counts c[0..BPT) of bins
+// (THREADS - 1 - t) * BPT + i, so thread 0 owns the highest bins. Writes *out when the histogram holds at least k keys
+// (else *out keeps what the caller put there). Ends synchronised.
+template <int THREADS, int BPT>
+__device__ __forceinline__ void first_digit(const uint32_t (&c)[BPT], uint32_t k, uint32_t (*wave_tot)[2],
+                                            uint32_t* out) {
+    const int rt = THREADS - 1 - (int)threadIdx.x;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) sum += c[i];
+    uint32_t above, unused, tot, unused_tot;
+    block_scan2<THREADS>(sum, 0u, above, unused, tot, unused_tot, wave_tot);
+#pragma unroll
+    for (int i = BPT - 1; i >= 0; --i) {
+        if (above < k && above + c[i] >= k) *out = (uint32_t)(rt * BPT + i);
+        above += c[i];
+    }
+    __syncthreads();
+}
+
+// This thread's 16 scores of the tile as raw floats; positions at or past M are not read.
+__device__ __forceinline__ int load_tile_scores(const float* s, int i0, int M, float (&v)[kTileKPT]) {
+    const int nvalid = max(0, min(kTileKPT, M - i0));
+    if (nvalid == kTileKPT && (reinterpret_cast<uintptr_t>(s + i0) & 15) == 0) {
+#pragma unroll
+        for (int q = 0; q < kTileKPT / 4; ++q) {
+            const float4 f = *reinterpret_cast<const float4*>(s + i0 + 4 * q);
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kTileKPT; ++i) v[i] = i < nvalid ? s[i0 + i] : 0.0f;
+    }
+    return nvalid;
+}
+
+__global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, TiledArgs t) {
+    __shared__ uint32_t wave_tot[kTileThreads / 64][2];
+    __shared__ uint32_t sh_b1;
+    constexpr int kBPT = kHistBins / kTileThreads;   // 8 histogram bins per thread
+    // the tiles of one row go to one XCD (workgroups are dealt to the 8 XCDs round robin), so the row's histogram
+    // is fetched into that XCD's L2 once
+    int lin = blockIdx.x;
+    if ((gridDim.x & 7) == 0) lin = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    const int row = lin / t.T, tile = lin - row * t.T;
+    const int tid = threadIdx.x;
+    const float* s = a.scores + (size_t)row * a.score_stride;
+    const int i0 = tile * kTileKeys + tid * kTileKPT;
+    float v[kTileKPT];
+    const int nvalid = load_tile_scores(s, i0, a.M, v);
+    const int rt = kTileThreads - 1 - tid;
+    const uint4* gh = reinterpret_cast<const uint4*>(a.hist + (size_t)row * kSelectStateWords + rt * kBPT);
+    const uint4 h0 = gh[0], h1 = gh[1];
+    if (tid == 0) sh_b1 = 0u;
+    const uint32_t c[kBPT] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    first_digit<kTileThreads, kBPT>(c, (uint32_t)a.k, wave_tot, &sh_b1);
+    const uint32_t b1 = sh_b1;
+    uint32_t abits = 0, cbits = 0;
+#pragma unroll
+    for (int i = 0; i < kTileKPT; ++i) {
+        const uint32_t dg = score_key(v[i]) >> kHistShift;
+        if (i < nvalid) {
+            abits |= (uint32_t)(dg > b1) << i;
+            cbits |= (uint32_t)(dg == b1) << i;
+        }
+    }
+    // two threads per 32-bit word: the even thread's keys are the low half
+    const uint32_t an = __shfl_xor(abits, 1, 64), cn = __shfl_xor(cbits, 1, 64);
+    const int w = tile * (kTileKeys / 32) + (tid >> 1);
+    if ((tid & 1) == 0 && w < t.W) {
+        t.above[(size_t)row * t.W + w] = abits | (an << 16);
+        t.cand[(size_t)row * t.W + w] = cbits | (cn << 16);
+    }
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, TiledArgs t) {
+    __shared__ SelectShared sh;                 // sortbuf holds the candidate list (as uint32 indices)
+    __shared__ uint32_t hist3[1024];
+    __shared__ uint32_t bits[kMaxWords];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int W = t.W;
+    const int wpt = (W + kSelThreads - 1) / kSelThreads;   // <= kMaxWordsPerThread
+    const int w0 = tid * wpt;
+    uint32_t cb[kMaxWordsPerThread], ab[kMaxWordsPerThread];
+#pragma unroll
+    for (int j = 0; j < kMaxWordsPerThread; ++j) {
+        const bool ok = j < wpt && w0 + j < W;
+        cb[j] = ok ? t.cand[(size_t)row * W + w0 + j] : 0u;
+        ab[j] = ok ? t.above[(size_t)row * W + w0 + j] : 0u;
+    }
+    for (int i = tid; i < kHistBins; i += kSelThreads) sh.hist[i] = 0u;
+    hist3[tid] = 0u;
+    if (tid == 0) {   // defaults keep every later index in range even for a state that does not match the scores
+        sh.digit = 0u;
+        sh.krem = 0u;
+    }
+    uint32_t nc = 0, na = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxWordsPerThread; ++j) {
+        if (j < wpt && w0 + j < W) bits[w0 + j] = ab[j];
+        nc += __popc(cb[j]);
+        na += __popc(ab[j]);
+    }
+    uint32_t ec, unused, n, n_above;
+    block_scan2<kSelThreads>(nc, na, ec, unused, n, n_above, sh.wave_tot);
+    if (n > (uint32_t)kCandCap) {   // too many keys share the threshold's first digit: single-workgroup select
+        select_row_streaming(a, row, sh);
+        return;
+    }
+    // candidate list in index order
+    uint32_t* list = reinterpret_cast<uint32_t*>(sh.sortbuf);
+    uint32_t pos = ec;
+#pragma unroll
+    for (int j = 0; j < kMaxWordsPerThread; ++j) {
+        uint32_t word = cb[j];
+        while (word) {
+            const uint32_t b = __ffs(word) - 1;
+            word &= word - 1;
+            if (pos < (uint32_t)kCandCap) list[pos] = (uint32_t)(w0 + j) * 32u + b;
+            ++pos;
+        }
+    }
+    __syncthreads();
+    // this thread's candidates: list entries [4 tid, 4 tid + 4), so ties rank in index order across threads
+    const float* srow = a.scores + (size_t)row * a.score_stride;
+    uint32_t cidx[kCandPerThread], low[kCandPerThread];
+    bool cv[kCandPerThread];
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) {
+        const uint32_t p = (uint32_t)(kCandPerThread * tid + i);
+        cv[i] = p < n;
+        cidx[i] = cv[i] ? min(list[p], (uint32_t)a.M - 1u) : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) low[i] = cv[i] ? score_key(srow[cidx[i]]) & 0x1fffffu : 0u;
+    // the candidates share the first digit: the threshold is found on the low 21 bits (digits of 11 and 10 bits)
+    uint32_t krem = (uint32_t)a.k - n_above;     // candidates to take, 1 <= krem <= n
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i)
+        if (cv[i]) atomicAdd(&sh.hist[low[i] >> 10], 1u);
+    __syncthreads();
+    find_digit(sh, sh.hist, krem, 2048);
+    const uint32_t d2 = sh.digit & 2047u;
+    krem = sh.krem;
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i)
+        if (cv[i] && (low[i] >> 10) == d2) atomicAdd(&hist3[low[i] & 1023u], 1u);
+    __syncthreads();
+    find_digit(sh, hist3, krem, 1024);
+    const uint32_t tlow = (d2 << 10) | (sh.digit & 1023u);
+    krem = sh.krem;
+    // equal keys at the threshold: the first krem of them in index order are taken
+    uint32_t neq = 0;
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) neq += cv[i] && low[i] == tlow;
+    uint32_t eeq, unused2, teq, unused_t2;
+    block_scan2<kSelThreads>(neq, 0u, eeq, unused2, teq, unused_t2, sh.wave_tot);
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) {
+        if (!cv[i]) continue;
+        const bool eq = low[i] == tlow;
+        if (low[i] > tlow || (eq && eeq < krem)) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
+        eeq += eq;
+    }
+    __syncthreads();
+    // emission: the set bits of this thread's words, in index order
+    uint32_t sw[kMaxWordsPerThread];
+    uint32_t ns = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxWordsPerThread; ++j) {
+        sw[j] = (j < wpt && w0 + j < W) ? bits[w0 + j] : 0u;
+        ns += __popc(sw[j]);
+    }
+    uint32_t slot, unused3, tsel, unused_t3;
+    block_scan2<kSelThreads>(ns, 0u, slot, unused3, tsel, unused_t3, sh.wave_tot);
+    const int nrec = a.legal - a.hi, S = a.lo + nrec + a.k, nf = a.lo + nrec;
+    int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride : nullptr;
+    int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S : nullptr;
+    const int64_t base = (int64_t)row * a.C;
+#pragma unroll
+    for (int j = 0; j < kMaxWordsPerThread; ++j) {
+        uint32_t word = sw[j];
+        while (word) {
+            const uint32_t b = __ffs(word) - 1;
+            word &= word - 1;
+            const int idx = (w0 + j) * 32 + (int)b;
+            if (slot < (uint32_t)a.k) {
+                if (rows) rows[a.lo + slot] = a.lo + idx;
+                if (flat) flat[a.lo + slot] = base + a.lo + idx;
+            }
+            ++slot;
+        }
+    }
+    for (int f = tid; f < nf; f += kSelThreads) {
+        const int p = f < a.lo ? f : a.hi + (f - a.lo);
+        const int s_out = f < a.lo ? f : a.lo + a.k + (f - a.lo);
+        if (rows) rows[s_out] = p;
+        if (flat) flat[s_out] = base + p;
+    }
+    uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
+    for (int i = tid; i < kHistBins; i += kSelThreads) st[i] = 0u;
+}
+
+static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s) {
+    hipLaunchKernelGGL(select_classify, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
+    hipLaunchKernelGGL(select_resolve, dim3(R), dim3(kSelThreads), 0, s, a, t);
+    return check_launch("select_tiled");
+}
+
+int64_t select_scratch_bytes(int R, int M) { return tiled_scratch_bytes(R, M); }
+
 int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
-                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* hist,
-                     hipStream_t stream) {
+                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                     void* scratch, int64_t scratch_bytes, hipStream_t stream) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
                     lo, hi, legal, C);
@@ -371,10 +627,22 @@ int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, in
     ATTNLAB_REQUIRE(S >= 1, "empty row list");
     ATTNLAB_REQUIRE(rows == nullptr || rows_stride >= S, "rows_stride=%lld smaller than S=%d", (long long)rows_stride, S);
     ATTNLAB_REQUIRE(k == 0 || (scores != nullptr && score_stride >= M), "scores must hold M=%d values per row", M);
-    if (!rows && !rows_flat && !hist) return ATTNLAB_OK;
+    ATTNLAB_REQUIRE(scratch_bytes >= 0, "negative scratch_bytes");
+    if (!rows && !rows_flat && !state) return ATTNLAB_OK;
+    const int R = B * G;
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
-                 hist};
-    return launch_select(a, B * G, stream);
+                 state};
+    const int W = (M + 31) / 32;
+    const bool tiled = state && scratch && k > 0 && order == ATTNLAB_ORDER_POSITION && W <= kMaxWords &&
+                       (reinterpret_cast<uintptr_t>(state) & 15) == 0 && (reinterpret_cast<uintptr_t>(scratch) & 3) == 0 &&
+                       scratch_bytes >= tiled_scratch_bytes(R, M);
+    if (!tiled) return launch_select(a, R, stream);
+    TiledArgs t;
+    t.above = static_cast<uint32_t*>(scratch);
+    t.cand = t.above + (size_t)R * W;
+    t.W = W;
+    t.T = (M + kTileKeys - 1) / kTileKeys;
+    return launch_tiled(a, t, R, stream);
 }
 
 }  // namespace attnlab
@@ -398,7 +666,12 @@ extern "C" int attnlab_topk(const float* scores, int64_t score_stride, int R, in
 
 extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal,
                                    int k, int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat,
-                                   uint32_t* hist, void* stream) {
-    return select_rows_impl(scores, score_stride, B, G, lo, hi, legal, k, C, order, rows, rows_stride, rows_flat, hist,
-                            reinterpret_cast<hipStream_t>(stream));
+                                   uint32_t* state, void* scratch, int64_t scratch_bytes, void* stream) {
+    return select_rows_impl(scores, score_stride, B, G, lo, hi, legal, k, C, order, rows, rows_stride, rows_flat, state,
+                            scratch, scratch_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t attnlab_select_scratch_bytes(int R, int M) {
+    if (R < 0 || M < 0) return -1;
+    return select_scratch_bytes(R, M);
 }

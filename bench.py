@@ -129,9 +129,11 @@ def launchers(ls, torch):
     ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     part = torch.empty(B * G * max(P, Pd) * h * 130, dtype=torch.float32, device=dev)
-    # top-k histograms: zero once; each score/select pair leaves them zeroed
-    step_hist = torch.zeros(B * G * nat.HIST_BINS, dtype=torch.int32, device=dev)
-    hist = torch.zeros(B * G * nat.HIST_BINS, dtype=torch.int32, device=dev)
+    # select state (top-k histograms and counters): zero once; each score/select pair leaves it zeroed
+    step_hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
+    hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
+    sel_bytes = lib.attnlab_select_scratch_bytes(B * G, ls.M)
+    sel_scratch = torch.empty(sel_bytes, dtype=torch.uint8, device=dev)
     u_buf = torch.zeros(B * G * r, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(d)
 
@@ -161,7 +163,8 @@ def launchers(ls, torch):
 
     def select(l):
         nat.call("attnlab_select_rows", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
-                 nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), stream())
+                 nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), sel_scratch.data_ptr(),
+                 sel_bytes, stream())
 
     def score_select(l):
         score(l)
@@ -174,7 +177,7 @@ def launchers(ls, torch):
 
     return {"sparse": sparse, "dense": dense, "score": score, "scan": scan, "select": select, "attend": attend,
             "score_select": score_select, "hist": hist, "partitions": P, "dense_partitions": Pd,
-            "_keep": (ws, part, step_hist, u_buf)}
+            "_keep": (ws, part, step_hist, u_buf, sel_scratch)}
 
 
 def kernel_breakdown(torch, fns, ls, reps):

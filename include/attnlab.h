@@ -39,6 +39,10 @@ extern "C" {
 #define ATTNLAB_DT_F16 1
 #define ATTNLAB_DT_F32 2
 
+/* Words per row of the select state shared by attnlab_score_grouped and attnlab_select_rows: the first-digit
+ * histogram (2048 bins), then reserved words, padded to 256 bytes. */
+#define ATTNLAB_SELECT_STATE_WORDS 2112
+
 /* ABI version; bumped on any signature change. */
 int attnlab_abi_version(void);
 
@@ -63,13 +67,14 @@ const char* attnlab_target(void);
  * Requires r <= 32, 0 <= lo <= hi <= C, 0 <= write_col < C and write_col outside [lo, hi) when k_new != NULL.
  * vector != 0 selects the 16-byte-load scan (used when C % 8 == 0 and zT is 16-byte aligned; otherwise the 2-byte
  * scan runs, the counterpart of the reference's v1 fallback, metal_score.py:289-292).
- * hist (nullable): [B*G, 2048] uint32, zero on entry; receives, per (b,g), the histogram of the scores' first radix
- * digit (top 11 bits of the order-preserving key), which attnlab_select_rows consumes and clears.
+ * state (nullable): select state [B*G, ATTNLAB_SELECT_STATE_WORDS] uint32, zero on entry; receives, per (b,g), the
+ * histogram of the scores' first radix digit (top 11 bits of the order-preserving key) in its first 2048 words, which
+ * attnlab_select_rows consumes and clears.
  */
 int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                           const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride,
                           int B, int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector,
-                          uint32_t* hist, void* stream);
+                          uint32_t* state, void* stream);
 
 /*
  * Prologue only: u (and the z column when k_new != NULL). The first launch of MetalScore.two_launch
@@ -119,12 +124,19 @@ int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k,
  * S = lo + (legal - hi) + k. rows: [B*G, S] int32 positions (row stride rows_stride; nullable). rows_flat: [B*G*S]
  * int64 flat row ids pos + (b*G+g)*C of the flattened [B*G*C, d] cache (sparse.py:14-16; nullable).
  * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE (the latter needs k <= 4096).
- * hist (nullable): the first-digit histograms attnlab_score_grouped built for these scores; when given, the first
- * radix pass is skipped and the histograms are left zeroed for the next call.
+ * state (nullable): the select state [B*G, ATTNLAB_SELECT_STATE_WORDS] attnlab_score_grouped filled for these scores;
+ * when given, the first radix pass is skipped and the state is left zeroed for the next call.
+ * scratch (nullable, 4-byte aligned, no zeroing needed): with state, position order, 0 < k, hi - lo <= 262144 and
+ * scratch_bytes >= attnlab_select_scratch_bytes(B*G, hi - lo), the keys are classified by a grid of 4096-key tiles
+ * and each row resolved by one workgroup (two launches) instead of one workgroup per row reading every key three
+ * times; the result is the same.
  */
 int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
-                        int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* hist,
-                        void* stream);
+                        int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                        void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Scratch bytes of the tiled select of attnlab_select_rows for R rows of M candidates (-1 for negative sizes). */
+int64_t attnlab_select_scratch_bytes(int R, int M);
 
 /*
  * Gather-free sparse attention. Replaces MetalAttend.__call__ (metal_attend.py:226-250, kernels :46-169) and the
@@ -151,29 +163,29 @@ int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_t kv_bg_str
                          int out_bf16, float* part, void* stream);
 
 /*
- * Workspace (bytes) of attnlab_sparse_decode_step for these sizes: candidate scores, row list and split-K partials,
- * each 256-byte aligned.
+ * Workspace (bytes) of attnlab_sparse_decode_step for these sizes: candidate scores, row list, u, tiled-select
+ * scratch and split-K partials, each 256-byte aligned. Its contents need no initialisation.
  */
 int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int legal, int k, int P);
 
 /*
  * One layer's sparse decode read for one new query: z column write, u projection, candidate scan, top-k, merge with
- * F, gather-free attention. Replaces sparse_decode_step_kernel (decode.py:145-163) with three or four launches on
- * `stream` (score, select, attend, and the split-K merge when P > 1). Calls sharing a workspace must be ordered on
- * one stream.
+ * F, gather-free attention. Replaces sparse_decode_step_kernel (decode.py:145-163) with a few launches on `stream`
+ * (score prologue and scan; select, tiled in two launches when `state` is given; attend, and the split-K merge
+ * when P > 1). Calls sharing a workspace or a select state must be ordered on one stream.
  * q_main: [B,G,h,128] bf16 (post-RoPE query); q_cat: [B,G,h*128] bf16 (pre-RoPE query, project_queries order);
  * K/V: [B,G,C,128] bf16; zT: [B,G,r,C] bf16; wq_t: [G,h*128,r]; wk: [G,r,128]; k_new: [B,G,128] (nullable: the
  * z column is not written). F = [0, lo) U [hi, legal); k top candidates; write_col = legal - 1 for the reference's
  * plan. rows_out: [B*G, S] int32 positions (nullable: kept in the workspace); rows_flat: [B*G*S] int64 flat ids
  * (nullable). out: [B,G,h,128] bf16. P: split-K partitions of the attend (1..64). order as in attnlab_select_rows.
- * hist: [B*G, 2048] uint32, zero before the first call; the score kernel fills it and the select kernel clears it,
- * so it stays zero between calls with no memset (the launches stay capturable in a HIP graph). Nullable: the
- * select kernel then runs its own first radix pass.
+ * state: select state [B*G, ATTNLAB_SELECT_STATE_WORDS] uint32, zero before the first call; the score kernel fills
+ * it and the select kernels clear it, so it stays zero between calls with no memset (the launches stay capturable in
+ * a HIP graph). Nullable: the select kernel then runs its own first radix pass on one workgroup per row.
  */
 int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K, const uint16_t* V,
                                uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk, const uint16_t* k_new,
                                int B, int G, int h, int r, int C, int lo, int hi, int legal, int k, int write_col,
-                               float scale, int order, int P, uint32_t* hist, void* workspace,
+                               float scale, int order, int P, uint32_t* state, void* workspace,
                                int64_t workspace_bytes, int32_t* rows_out, int64_t* rows_flat, uint16_t* out,
                                void* stream);
 

@@ -55,10 +55,22 @@ def test_invalid_arguments_are_rejected_before_any_launch(native_lib):
     with pytest.raises(ValueError, match="partitions"):
         _native.call("attnlab_dense_decode", 16, 16, 128 * 128, 128, 16, 1, 8, 2, 10, 128, 0, 0.1, 16, 1, None, None)
     with pytest.raises(ValueError, match="legal"):
-        _native.call("attnlab_select_rows", 16, 10, 1, 8, 4, 20, 10, 3, 100, 0, 16, 10, None, None, None)
+        _native.call("attnlab_select_rows", 16, 10, 1, 8, 4, 20, 10, 3, 100, 0, 16, 10, None, None, None, 0, None)
     with pytest.raises(ValueError, match="workspace"):
         _native.call("attnlab_sparse_decode_step", *([16] * 8), 1, 8, 2, 32, 4096, 4, 4032, 4096, 128, 4095, 0.1, 0, 4,
                      None, 256, 10, None, None, 16, None)
+
+
+def select_scratch(R, M):
+    """Tiled select scratch: two bitmaps of one bit per candidate (keys above the threshold's first digit, keys
+    sharing it), in 32-bit words."""
+    return R * 2 * 4 * ((M + 31) // 32)
+
+
+def test_select_scratch_formula(native_lib):
+    for R, M in ((128, 32704), (8, 1), (1, 4096), (1, 4097), (3, 0)):
+        assert native_lib.attnlab_select_scratch_bytes(R, M) == select_scratch(R, M)
+    assert native_lib.attnlab_select_scratch_bytes(-1, 5) == -1
 
 
 def test_workspace_size_formula(native_lib):
@@ -67,7 +79,8 @@ def test_workspace_size_formula(native_lib):
         BG, M, S = B * G, hi - lo, lo + (legal - hi) + k
         scores = a(BG * ((M + 3) // 4 * 4) * 4) if k > 0 else 0
         u = a(BG * 32 * 4) if k > 0 else 0
-        return scores + a(BG * S * 4) + u + (a(BG * P * h * 130 * 4) if P > 1 else 0)
+        sel = a(select_scratch(BG, M)) if k > 0 else 0
+        return scores + a(BG * S * 4) + u + sel + (a(BG * P * h * 130 * 4) if P > 1 else 0)
     for args in ((16, 8, 4, 4, 32704, 32768, 1024, 4), (1, 8, 2, 4, 1984, 2048, 64, 1), (2, 8, 2, 60, 60, 60, 0, 8)):
         assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)
     assert native_lib.attnlab_sparse_decode_workspace(0, 8, 2, 4, 100, 164, 3, 1) == -1

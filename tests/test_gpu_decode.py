@@ -191,7 +191,7 @@ def test_full_size_32k_b16_properties(gpu):
 
 
 def test_graph_replay_matches_eager(gpu):
-    """The three launches of a step captured in a HIP graph: every replay equals the eager result."""
+    """The launches of a step captured in a HIP graph: every replay equals the eager result."""
     K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=4, h=4, C=4096, seed=8)
     L = 4000
     req = prepare_request(4, 8, 4096, valid_length=L, query_position=L - 1, rho=1 / 32, device=gpu)

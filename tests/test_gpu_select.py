@@ -106,29 +106,104 @@ def test_select_rows_matches_oracle(gpu, legal, k0, order):
     assert np.array_equal(flat.cpu().numpy().reshape(B, G, S), want + off)
 
 
-@pytest.mark.parametrize("B,C,L,order", [(1, 2048 + 64, 2048, "position"), (4, 32768, 32768, "score"),
-                                         (2, 70000, 70000, "position"), (3, 1000, 777, "score")])
-def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order):
-    """score_grouped(hist=) + select_rows(hist=) gives exactly the rows of the self-contained select, leaves the
-    histogram zeroed, and stays exact over repeated calls on fresh data (a stale histogram would break it)."""
+@pytest.mark.parametrize("B,C,L,order,tiled", [(1, 2048 + 64, 2048, "position", True), (4, 32768, 32768, "score", True),
+                                               (2, 70000, 70000, "position", True), (3, 1000, 777, "score", True),
+                                               (2, 32768, 32768, "position", False)])
+def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order, tiled):
+    """score_grouped(state=) + select_rows(state=) gives exactly the rows of the self-contained select, leaves the
+    state zeroed, and stays exact over repeated calls on fresh data (a stale histogram would break it)."""
+    from attention_lab import _native as nat
     from attention_lab import hip_score
     from oracle import rules
     G, r = 8, 32
     lo, hi, k, S = rules.step(L, rules.budget(L, 1 / 32))
-    hist = torch.zeros(B, G, 2048, dtype=torch.int32, device=gpu)
+    state = torch.zeros(B, G, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
     for rep in range(3):
         gen = torch.Generator().manual_seed(100 * rep + B)
         zT = torch.randn(B, G, r, C, generator=gen).to(torch.bfloat16).to(gpu)
         u = torch.randn(B, G, r, generator=gen).to(gpu)
-        s = hip_score.score_grouped(zT, lo, hi, u=u, hist=hist)
-        rows_h, _ = hip_select.select_rows(s, lo, hi, L, k, C, order=order, hist=hist)
+        s = hip_score.score_grouped(zT, lo, hi, u=u, state=state)
+        rows_h, _ = hip_select.select_rows(s, lo, hi, L, k, C, order=order, state=state, tiled=tiled)
         torch.cuda.synchronize()
-        assert int(hist.abs().sum()) == 0, "the select kernel must leave the histogram zeroed"
+        assert int(state.abs().sum()) == 0, "the select kernels must leave the state zeroed"
         rows_p, _ = hip_select.select_rows(s, lo, hi, L, k, C, order=order)
         torch.cuda.synchronize()
         assert torch.equal(rows_h, rows_p)
         want = exact.select_rows(s.cpu().numpy(), lo, hi, L, k, order=order)
         assert np.array_equal(rows_h.cpu().numpy(), want)
+
+
+def score_keys(s):
+    """Order-preserving uint32 keys of fp32 scores: NaN -> 0, -0.0 -> +0.0, negative -> bitwise not, else sign set."""
+    u = np.ascontiguousarray(s, dtype=np.float32).view(np.uint32).copy()
+    u[u == 0x80000000] = 0
+    key = np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint32)
+    key[np.isnan(s)] = 0
+    return key
+
+
+def state_for(s):
+    """Select state [B, G, 2112] whose histogram is that of the scores' first 11-bit digit (counter word zero)."""
+    from attention_lab import _native as nat
+    B, G, M = s.shape
+    st = np.zeros((B, G, nat.SELECT_STATE_WORDS), dtype=np.int64)
+    d = (score_keys(s) >> 21).astype(np.int64)
+    for b in range(B):
+        for g in range(G):
+            st[b, g, :2048] = np.bincount(d[b, g], minlength=2048)
+    return torch.from_numpy(st.astype(np.int32))
+
+
+def tie_heavy(rng, shape):
+    return rng.integers(0, 6, size=shape).astype(np.float32) * 0.25
+
+
+def specials(rng, shape):
+    s = rng.standard_normal(shape).astype(np.float32)
+    m = rng.random(shape)
+    s[m < 0.05] = np.nan
+    s[(m >= 0.05) & (m < 0.1)] = -0.0
+    s[(m >= 0.1) & (m < 0.15)] = 0.0
+    s[(m >= 0.15) & (m < 0.17)] = np.inf
+    s[(m >= 0.17) & (m < 0.19)] = -np.inf
+    return s
+
+
+@pytest.mark.parametrize("M,k,gen", [(1, 1, "normal"), (3, 2, "normal"), (1000, 31, "normal"), (1024, 1024, "normal"),
+                                     (1025, 32, "normal"), (4096, 128, "normal"), (4097, 129, "normal"),
+                                     (8191, 4000, "normal"), (32704, 1024, "normal"), (262145, 8192, "normal"), (70000, 2187, "normal"),
+                                     (3000, 100, "ties"), (32704, 1024, "ties"), (20000, 600, "specials"),
+                                     (32704, 32704, "normal"), (5000, 4999, "ties")])
+def test_tiled_select_matches_the_oracle(gpu, M, k, gen):
+    """Tiled select (4096-key tiles classified, one workgroup per row resolves) vs the oracle: plain, ties at the
+    threshold (taken in index order), more than 4096 candidates sharing the threshold's first digit
+    (single-workgroup fallback), NaN / +-0 / +-inf, k = M, a row too long for the tiled path (262144 < M); the state
+    is left zeroed and a second call on other data is exact too."""
+    rng = np.random.default_rng(M + k)
+    B, G = 2, 3
+    lo = 5
+    hi = lo + M
+    legal = hi + 7
+    C = legal + 3
+    state = None
+    for rep in range(2):
+        shape = (B, G, M)
+        s = {"normal": lambda: rng.standard_normal(shape).astype(np.float32),
+             "ties": lambda: tie_heavy(rng, shape), "specials": lambda: specials(rng, shape)}[gen]()
+        st = state_for(s).to(gpu)
+        if state is None:
+            state = st
+        else:
+            assert int(state.abs().sum()) == 0
+            state.copy_(st)
+        t = torch.from_numpy(s).to(gpu)
+        rows, flat = hip_select.select_rows(t, lo, hi, legal, k, C, order="position", want_flat=True, state=state)
+        torch.cuda.synchronize()
+        want = exact.select_rows(s, lo, hi, legal, k, order="position")
+        assert np.array_equal(rows.cpu().numpy(), want), f"rep {rep}"
+        off = (np.arange(B * G) * C).reshape(B, G, 1)
+        assert np.array_equal(flat.cpu().numpy().reshape(B, G, -1), want + off)
+        assert int(state.abs().sum()) == 0, "the tiled select must leave the state zeroed"
 
 
 def test_validation(gpu):
