@@ -7,11 +7,13 @@
 // Layout per workgroup (256 threads = 4 waves) of one (b, g, partition): 8 lanes share a position; lane `sub` owns
 // dims [8*sub, 8*sub+8) and [64+8*sub, 64+8*sub+8), so one 16-byte load per lane and half-row covers 128 contiguous
 // bytes (one cache line) and a wave reads 8 positions per load instruction. The 32 position slots of the block walk
-// the partition with stride 32, R positions per iteration, all R K/V loads issued before any arithmetic. q . k is a
+// the partition with stride 32, R positions per iteration, software-pipelined over two register sets: the row
+// indices of iteration i+2 and the K/V rows of iteration i+1 are in flight while iteration i is computed. q . k is a
 // bf16 dot2 (v_dot2_f32_bf16, fp32 accumulate) finished by a 3-step DPP sum over the 8 lanes; every head of the group
 // reuses the same K and V registers (GQA sharing). Online softmax runs in the log2 domain with a lazy rescale: the
 // running max is raised only when a block max exceeds it by more than 2^8, so the 16*h accumulator rescale is rare.
-// Slots are merged with DPP/shuffles and LDS. With P > 1 partitions every block writes its (m, l, acc) partial and a
+// Slots are merged with DPP (lane ^ 8) and v_permlane16/32_swap (lane ^ 16, ^ 32), then the 4 waves through LDS.
+// With P > 1 partitions every block writes its (m, l, acc) partial and a
 // second small kernel merges them; the kernel boundary is what makes the partials of other XCDs' L2s visible, which
 // is far cheaper on this part than a device-scope fence per block.
 #include "common.h"
@@ -22,6 +24,7 @@ constexpr int kHeadDim = 128;
 constexpr int kAttThreads = 256;
 constexpr int kSlots = kAttThreads / 8;  // positions in flight per block per step
 constexpr float kLazyRescale = 8.0f;     // log2-domain slack of the running max
+constexpr int kStages = 4;               // K/V groups in flight per wave (LDS stages)
 
 struct AttendArgs {
     const uint16_t* K;
@@ -53,14 +56,79 @@ __device__ __forceinline__ void store_out(const AttendArgs& a, size_t idx, float
     else reinterpret_cast<float*>(a.out)[idx] = v;
 }
 
-template <int H, int R, bool DENSE>
+// Exchange with lane ^ 16 (SWAP16) or lane ^ 32 and merge, one head at a time: v_permlane16/32_swap hand every lane
+// of a pair both values, lower lane first, so both lanes compute the same merge from the same operands in the same
+// order and end with bit-identical state.
+template <int H, bool SWAP16>
+__device__ __forceinline__ void merge_across(float (&m)[H], float (&l)[H], float (&acc)[H][16]) {
+    auto swap = [](float x, float& lo, float& hi) {
+        const uint32_t u = __float_as_uint(x);
+        if constexpr (SWAP16) {
+            const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            lo = __uint_as_float(r[0]);
+            hi = __uint_as_float(r[1]);
+        } else {
+            const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            lo = __uint_as_float(r[0]);
+            hi = __uint_as_float(r[1]);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        float ma, mb, la, lb;
+        swap(m[i], ma, mb);
+        swap(l[i], la, lb);
+        const float mn = fmaxf(ma, mb);
+        const float w1 = (ma == -INFINITY) ? 0.0f : fast_exp2(ma - mn);
+        const float w2 = (mb == -INFINITY) ? 0.0f : fast_exp2(mb - mn);
+        m[i] = mn;
+        l[i] = w1 * la + w2 * lb;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float xa, xb;
+            swap(acc[i][e], xa, xb);
+            acc[i][e] = w1 * xa + w2 * xb;
+        }
+    }
+}
+
+// s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding. Loads complete in issue order, so
+// this is how the kernel knows that the LDS copies of an older stage have landed (the compiler does not track the LDS
+// writes of global_load_lds).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The four 16-byte LDS words of this lane in a stage (K lo, K hi, V lo, V hi at 1 KiB spacing), read in inline
+// assembly: a plain LDS read of memory that global_load_lds also writes makes the compiler wait for every outstanding
+// load (vmcnt(0)), which would serialise the pipeline; the caller's wait_vmcnt is what orders these reads.
+__device__ __forceinline__ void read_stage(const uint4* st_lane, u32x4_t& k0, u32x4_t& k1, u32x4_t& v0, u32x4_t& v1) {
+    const uint32_t addr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint4*)st_lane;
+    asm volatile(
+        "ds_read_b128 %0, %4\n"
+        "ds_read_b128 %1, %4 offset:1024\n"
+        "ds_read_b128 %2, %4 offset:2048\n"
+        "ds_read_b128 %3, %4 offset:3072\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=v"(k0), "=v"(k1), "=v"(v0), "=v"(v1)
+        : "v"(addr)
+        : "memory");
+}
+
+template <int H, int D, bool DENSE>
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
+    constexpr int kChunk = 1024;   // row-list entries whose positions are staged in LDS at a time
+    __shared__ __attribute__((aligned(16))) uint4 stage[4][D][4][64];   // [wave][stage][K lo, K hi, V lo, V hi][lane]
+    __shared__ int idx_sh[DENSE ? 1 : kChunk];
     __shared__ float red_ml[4][H][2];
-    __shared__ float red_acc[4][H][kHeadDim];
+    static_assert(sizeof(float) * 4 * H * kHeadDim <= sizeof(uint4) * 4 * D * 4 * 64, "wave merge buffer");
+    float (*red_acc)[H][kHeadDim] = reinterpret_cast<float (*)[H][kHeadDim]>(&stage[0][0][0][0]);
     const int bg = blockIdx.x / a.P;
     const int p = blockIdx.x - bg * a.P;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = (wave << 3) | (lane >> 3);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slot = lane >> 3;
     const int sub = lane & 7;
     const int h = a.h;
 
@@ -93,63 +161,64 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
     }
 
-    for (int s0 = s_begin + slot; s0 < s_end; s0 += kSlots * R) {
-        bool ok[R];
-        uint4 k0[R], k1[R], v0[R], v1[R];
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-            const int s = s0 + kSlots * t;
-            bool okt = s < s_end;
-            int pos = 0;
-            if (okt) {
-                pos = DENSE ? s : rl[s];
-                if (!DENSE) okt = (unsigned)pos < (unsigned)a.C;
-            }
-            ok[t] = okt;
-            k0[t] = k1[t] = v0[t] = v1[t] = make_uint4(0, 0, 0, 0);
-            if (okt) {
-                const size_t off = (size_t)pos * a.kv_row_stride;
-                k0[t] = *reinterpret_cast<const uint4*>(Kb + off);
-                k1[t] = *reinterpret_cast<const uint4*>(Kb + off + 64);
-                v0[t] = *reinterpret_cast<const uint4*>(Vb + off);
-                v1[t] = *reinterpret_cast<const uint4*>(Vb + off + 64);
-            }
+    const int chunk = DENSE ? max(s_end - s_begin, 1) : kChunk;
+    for (int c0 = s_begin; c0 < s_end; c0 += chunk) {
+        const int clen = min(chunk, s_end - c0);
+        if (!DENSE) {
+            __syncthreads();   // every wave is done with the previous chunk's positions
+            for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = rl[c0 + i];
+            __syncthreads();
         }
-        float sc[R][H];
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
+        // The chunk's entries form groups of 8 (one per slot of a wave); wave w takes groups w, w + 4, ...
+        const int ng = (clen + 7) / 8;
+        const int my_ng = ng > wave ? (ng - wave + 3) / 4 : 0;
+        // Stage j of this wave <- K/V rows of its j-th group: four 16-byte loads per lane straight into LDS, lane l's
+        // bytes at lane offset 16 l. Entries past the chunk or outside [0, C) load row 0 (in bounds) and are masked
+        // in compute, so every group issues exactly four loads.
+        auto issue = [&](int j) {
+            const int e = (wave + 4 * j) * 8 + slot;
+            int pos = 0;
+            if (e < clen) {
+                pos = DENSE ? c0 + e : idx_sh[e];
+                if (!DENSE && (unsigned)pos >= (unsigned)a.C) pos = 0;
+            }
+            const size_t off = (size_t)pos * a.kv_row_stride;
+            uint4* st = &stage[wave][j % D][0][0];
+            __builtin_amdgcn_global_load_lds(Kb + off, st, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Kb + off + 64, st + 64, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vb + off, st + 128, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vb + off + 64, st + 192, 16, 0, 0);
+        };
+        auto compute = [&](int j) {
+            const int e = (wave + 4 * j) * 8 + slot;
+            bool ok = e < clen;
+            if (!DENSE && ok) ok = (unsigned)idx_sh[e] < (unsigned)a.C;
+            u32x4_t k0, k1, v0, v1;
+            read_stage(&stage[wave][j % D][0][lane], k0, k1, v0, v1);
+            float sc[H];
 #pragma unroll
             for (int i = 0; i < H; ++i) {
                 float d = 0.0f;
-                d = dot2_bf16(qw[i][0], k0[t].x, d);
-                d = dot2_bf16(qw[i][1], k0[t].y, d);
-                d = dot2_bf16(qw[i][2], k0[t].z, d);
-                d = dot2_bf16(qw[i][3], k0[t].w, d);
-                d = dot2_bf16(qw[i][4], k1[t].x, d);
-                d = dot2_bf16(qw[i][5], k1[t].y, d);
-                d = dot2_bf16(qw[i][6], k1[t].z, d);
-                d = dot2_bf16(qw[i][7], k1[t].w, d);
+                d = dot2_bf16(qw[i][0], k0.x, d);
+                d = dot2_bf16(qw[i][1], k0.y, d);
+                d = dot2_bf16(qw[i][2], k0.z, d);
+                d = dot2_bf16(qw[i][3], k0.w, d);
+                d = dot2_bf16(qw[i][4], k1.x, d);
+                d = dot2_bf16(qw[i][5], k1.y, d);
+                d = dot2_bf16(qw[i][6], k1.z, d);
+                d = dot2_bf16(qw[i][7], k1.w, d);
                 d = sum8(d);
-                sc[t][i] = ok[t] ? d * a.scale_log2 : -INFINITY;
+                sc[i] = ok ? d * a.scale_log2 : -INFINITY;
+                if (sc[i] > m[i] + kLazyRescale) {
+                    const float al = fast_exp2(m[i] - sc[i]);
+                    l[i] *= al;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) acc[i][q] *= al;
+                    m[i] = sc[i];
+                }
             }
-        }
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-            float mb = sc[0][i];
-#pragma unroll
-            for (int t = 1; t < R; ++t) mb = fmaxf(mb, sc[t][i]);
-            if (mb > m[i] + kLazyRescale) {
-                const float al = fast_exp2(m[i] - mb);
-                l[i] *= al;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][e] *= al;
-                m[i] = mb;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
             float vf[16];
-            const uint32_t vw[8] = {v0[t].x, v0[t].y, v0[t].z, v0[t].w, v1[t].x, v1[t].y, v1[t].z, v1[t].w};
+            const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
             for (int w = 0; w < 8; ++w) {
                 vf[2 * w] = bf16_lo(vw[w]);
@@ -157,31 +226,38 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < H; ++i) {
-                const float pr = ok[t] ? fast_exp2(sc[t][i] - m[i]) : 0.0f;
+                const float pr = ok ? fast_exp2(sc[i] - m[i]) : 0.0f;
                 l[i] += pr;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][e] += pr * vf[e];
+                for (int q = 0; q < 16; ++q) acc[i][q] += pr * vf[q];
             }
+        };
+        const int pro = min(D - 1, my_ng);
+        for (int j = 0; j < pro; ++j) issue(j);
+        for (int j = 0; j < my_ng; ++j) {
+            if (j + D - 1 < my_ng) {
+                asm volatile("" ::: "memory");   // the stage refilled below was read by compute(j - 1)
+                issue(j + D - 1);
+                wait_vmcnt<4 * (D - 1)>();        // group j's four loads are older than the 4 (D - 1) after them
+            } else {
+                wait_vmcnt<0>();
+            }
+            compute(j);
         }
     }
 
-    // merge the 8 slots of the wave (lanes with equal `sub`): xor 8 (DPP row_ror:8), xor 16, xor 32
+    // merge the 8 slots of the wave (lanes with equal `sub`): xor 8 (DPP row_ror:8), then xor 16 and xor 32
 #pragma unroll
     for (int i = 0; i < H; ++i) {
+        float m2 = dpp_f32<0x128>(m[i]), l2 = dpp_f32<0x128>(l[i]);
+        float w1, w2;
+        merge_state(m[i], l[i], m2, l2, w1, w2);
 #pragma unroll
-        for (int step = 0; step < 3; ++step) {
-            float m2, l2;
-            if (step == 0) { m2 = dpp_f32<0x128>(m[i]); l2 = dpp_f32<0x128>(l[i]); }
-            else { m2 = shfl_xor_f32(m[i], step == 1 ? 16 : 32); l2 = shfl_xor_f32(l[i], step == 1 ? 16 : 32); }
-            float w1, w2;
-            merge_state(m[i], l[i], m2, l2, w1, w2);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float o = (step == 0) ? dpp_f32<0x128>(acc[i][e]) : shfl_xor_f32(acc[i][e], step == 1 ? 16 : 32);
-                acc[i][e] = w1 * acc[i][e] + w2 * o;
-            }
-        }
+        for (int e = 0; e < 16; ++e) acc[i][e] = w1 * acc[i][e] + w2 * dpp_f32<0x128>(acc[i][e]);
     }
+    merge_across<H, true>(m, l, acc);
+    merge_across<H, false>(m, l, acc);
+    __syncthreads();   // the wave merge buffer overlays the stages of every wave
     if (lane < 8) {
 #pragma unroll
         for (int i = 0; i < H; ++i) {
@@ -197,7 +273,6 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         }
     }
     __syncthreads();
-
     // merge the 4 waves: thread -> (head, dim) pairs
     for (int idx = tid; idx < h * kHeadDim; idx += kAttThreads) {
         const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
@@ -225,22 +300,42 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     }
 }
 
-// Merge the P partials of every (b, g): thread -> (head, dim).
+// Merge the P partials of every (b, g): thread -> (head, dim). Partials are read eight at a time, all loads of a group
+// issued before any is used, with an online rescale between groups.
 __global__ __launch_bounds__(1024) void attend_combine(AttendArgs a) {
+    constexpr int kGroup = 8;
     const int bg = blockIdx.x;
     const int h = a.h;
     const float* pb = a.part + (size_t)bg * a.P * h * (kHeadDim + 2);
     for (int idx = threadIdx.x; idx < h * kHeadDim; idx += blockDim.x) {
         const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
-        float ms = -INFINITY;
-        for (int q = 0; q < a.P; ++q) ms = fmaxf(ms, pb[((size_t)q * h + i) * (kHeadDim + 2)]);
-        float ls = 0.0f, as = 0.0f;
-        for (int q = 0; q < a.P; ++q) {
-            const float* pp = pb + ((size_t)q * h + i) * (kHeadDim + 2);
-            const float mw = pp[0];
-            const float ww = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - ms);
-            ls += ww * pp[1];
-            as += ww * pp[2 + dim];
+        float ms = -INFINITY, ls = 0.0f, as = 0.0f;
+        for (int q0 = 0; q0 < a.P; q0 += kGroup) {
+            float mv[kGroup], lv[kGroup], av[kGroup];
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                mv[u] = -INFINITY;
+                lv[u] = av[u] = 0.0f;
+                if (q0 + u < a.P) {
+                    const float* pp = pb + ((size_t)(q0 + u) * h + i) * (kHeadDim + 2);
+                    mv[u] = pp[0];
+                    lv[u] = pp[1];
+                    av[u] = pp[2 + dim];
+                }
+            }
+            float mn = ms;
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) mn = fmaxf(mn, mv[u]);
+            const float w0 = (ms == -INFINITY) ? 0.0f : fast_exp2(ms - mn);
+            ls *= w0;
+            as *= w0;
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                const float w = (mv[u] == -INFINITY) ? 0.0f : fast_exp2(mv[u] - mn);
+                ls += w * lv[u];
+                as += w * av[u];
+            }
+            ms = mn;
         }
         store_out(a, ((size_t)bg * h + i) * kHeadDim + dim, as / ls);
     }
@@ -249,10 +344,10 @@ __global__ __launch_bounds__(1024) void attend_combine(AttendArgs a) {
 template <bool DENSE>
 static int launch_attend(const AttendArgs& a, int BG, hipStream_t s) {
     const dim3 grid(BG * a.P), block(kAttThreads);
-    if (a.h <= 1) hipLaunchKernelGGL((attend_kernel<1, 4, DENSE>), grid, block, 0, s, a);
-    else if (a.h <= 2) hipLaunchKernelGGL((attend_kernel<2, 4, DENSE>), grid, block, 0, s, a);
-    else if (a.h <= 4) hipLaunchKernelGGL((attend_kernel<4, 4, DENSE>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attend_kernel<8, 2, DENSE>), grid, block, 0, s, a);
+    if (a.h <= 1) hipLaunchKernelGGL((attend_kernel<1, kStages, DENSE>), grid, block, 0, s, a);
+    else if (a.h <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE>), grid, block, 0, s, a);
+    else if (a.h <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attend_kernel<8, kStages, DENSE>), grid, block, 0, s, a);
     if (a.P > 1) hipLaunchKernelGGL(attend_combine, dim3(BG), dim3(a.h * kHeadDim), 0, s, a);
     return check_launch(DENSE ? "dense_decode" : "attend");
 }

@@ -124,8 +124,8 @@ def launchers(ls, torch):
     lib = nat.lib()
     dev = ls.K[0].device
     B, G, h, d, r, C = ls.B, ls.G, ls.h, ls.d, ls.r, ls.C
-    P = hip_attend.auto_partitions(B * G, ls.S, max_p=hip_attend.MAX_P, min_rows=64)
-    Pd = hip_attend.auto_partitions(B * G, ls.L, max_p=hip_attend.MAX_P_DENSE, min_rows=256)
+    P = hip_attend.sparse_partitions(B * G, ls.S)
+    Pd = hip_attend.dense_partitions(B * G, ls.L)
     ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     part = torch.empty(B * G * max(P, Pd) * h * 130, dtype=torch.float32, device=dev)

@@ -46,8 +46,12 @@ def run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical, n0=None
 
 
 def kernel_scores(zT, q_pre, idx, lo, hi):
+    """Scores exactly as the fused step computes them: u by the prologue kernel, then the scan from u (the same fp32
+    summation order, so the step's selection can be checked bit-exact against the oracle's on these scores)."""
     B, G, h, _, d = q_pre.shape
-    s = hip_score.score_grouped(zT, lo, hi, q_cat=q_pre.reshape(B, G, h * d).contiguous(), wq_t=idx.wq_t_scaled)
+    u_out = torch.empty(B, G, idx.wq_t_scaled.shape[-1], dtype=torch.float32, device=zT.device)
+    s = hip_score.score_grouped(zT, lo, hi, q_cat=q_pre.reshape(B, G, h * d).contiguous(), wq_t=idx.wq_t_scaled,
+                                u_out=u_out)
     torch.cuda.synchronize()
     return s.cpu().numpy()
 
