@@ -57,7 +57,89 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 per-layer figures")
     ap.add_argument("--kernel-reps", type=int, default=20, help="graph replays per kernel-average measurement")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="short run for rocprofv3 --pmc passes: 5 scan launches of one layer at the bench shape, then "
+                         "5 plain 256 MiB device copies that calibrate the counters; prints one JSON line")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise the counter_collection.csv files of a FETCH_SIZE pass and a WRITE_SIZE pass of "
+                         "--pmc-workload into HBM bytes per scan launch (no GPU needed)")
     return ap.parse_args()
+
+
+PMC_COPY_BYTES = 256 << 20
+PMC_PROFILE = os.path.join(ROOT, "profiles", "score_scan_v16_b16_l32k_pmc.md")
+SCAN_KERNEL = "score_scan_v16"
+
+
+def pmc_workload(torch, dev, args):
+    ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,
+                    layers=1, r=args.index_dim, rho=args.rho, seed=args.seed)
+    fns = launchers(ls, torch)
+    fns["score"](0)            # u for the scan launches
+    torch.cuda.synchronize()
+    for _ in range(5):
+        fns["scan"](0)
+    src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_workload": "score_scan_v16 x5 then 256 MiB copy x5", "scan_algorithmic_bytes": ls.scan_bytes(),
+                      "scan_read_bytes": ls.B * ls.G * ls.r * ls.M * 2, "scan_write_bytes": ls.B * ls.G * 4 * ls.M,
+                      "copy_bytes_each_way": PMC_COPY_BYTES}))
+    return 0
+
+
+def _counter_means(directory, counter):
+    """Mean counter value per dispatch for the scan kernel and for the calibration copy (torch's copy_ of 256 MiB runs
+    as the runtime's __amd_rocclr_copyBuffer kernel; its small set-up copies are told apart by the counter value)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    vals = {"scan": [], "copy": []}
+    with open(files[0], newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            name = row.get("Kernel_Name", "")
+            if SCAN_KERNEL in name:
+                vals["scan"].append(float(row["Counter_Value"]))
+            elif "copyBuffer" in name:
+                vals["copy"].append(float(row["Counter_Value"]))
+    big = max(vals["copy"], default=0.0)
+    vals["copy"] = [v for v in vals["copy"] if v >= 0.5 * big]
+    if not vals["scan"] or not vals["copy"]:
+        raise SystemExit(f"{counter}: found {len(vals['scan'])} scan and {len(vals['copy'])} copy dispatches")
+    return {k: sum(v) / len(v) for k, v in vals.items()}, {k: len(v) for k, v in vals.items()}
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the scan, each scaled by bytes / counter of the 256 MiB copy."""
+    fetch, nf = _counter_means(fetch_dir, "FETCH_SIZE")
+    write, nw = _counter_means(write_dir, "WRITE_SIZE")
+    f_scale = PMC_COPY_BYTES / (fetch["copy"] * 1024)
+    w_scale = PMC_COPY_BYTES / (write["copy"] * 1024)
+    read_b = fetch["scan"] * 1024 * f_scale
+    write_b = write["scan"] * 1024 * w_scale
+    out = {"fetch_kib_scan": fetch["scan"], "fetch_kib_copy": fetch["copy"], "fetch_scale": f_scale,
+           "write_kib_scan": write["scan"], "write_kib_copy": write["copy"], "write_scale": w_scale,
+           "dispatches": {"fetch": nf, "write": nw}, "traffic_read_bytes": read_b, "traffic_write_bytes": write_b,
+           "traffic_bytes_per_launch": read_b + write_b}
+    print(json.dumps(out, indent=1))
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per scan launch recorded by the committed rocprofv3 --pmc summary, or None."""
+    import re
+    try:
+        with open(PMC_PROFILE, encoding="utf-8") as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", f.read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 # ---------------------------------------------------------------------------------------------------------------------
@@ -303,6 +385,8 @@ def run_b1(torch, dev, args):
 
 def main() -> int:
     args = parse_args()
+    if args.pmc_summary:
+        return pmc_summary(*args.pmc_summary)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one GPU, and the "
                                    "multi-GPU design (tensor parallel by KV group) is described in DESIGN.md, not run",
@@ -316,6 +400,8 @@ def main() -> int:
     _native.lib()
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.pmc_workload:
+        return pmc_workload(torch, dev, args)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,
@@ -371,8 +457,9 @@ def main() -> int:
                    "batch": ls.B, "context": ls.L, "layers": ls.n, "kv_groups": ls.G, "heads_per_group": ls.h,
                    "head_dim": ls.d, "index_dim": ls.r, "rho": args.rho, "k": ls.k, "selected_rows": ls.S,
                    "global_batch": ls.B, "seq_len": ls.L, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "score_scan_vec (candidate scan of the index table)", "achieved": ach,
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS, "traffic": None,
+        "roofline": {"bound": "hbm", "kernel": f"{SCAN_KERNEL} (candidate scan of the index table)", "achieved": ach,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
+                     "traffic": measured_traffic() if (ls.B, ls.L, ls.G, ls.r) == (16, 32768, 8, 32) else None,
                      "algorithmic_bytes_per_launch": scan_b, "avg_launch_us": kus["scan"]},
         "per_layer_us": {"sparse": us_layer, "dense": ms_dense * 1e3 / ls.n, "score_prologue_and_scan": score_us,
                          "scan": kus["scan"], "select": kus["select"], "attend_with_combine": kus["attend"]},
