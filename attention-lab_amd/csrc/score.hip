@@ -33,6 +33,7 @@ struct ScoreArgs {
 };
 
 constexpr int kMaxR = 32;
+constexpr int kMaxHd = 1024;   // q_cat features (h * d, h <= 8) whose u loads are all issued at once
 
 // u[j] = sum_f q_cat[f] * wq_t[f, j] for one (b, g), reduced into u_sh[0..r). Uses `red` (BLOCK/64 x 32 floats).
 template <int BLOCK>
@@ -41,18 +42,43 @@ __device__ __forceinline__ void build_u(const ScoreArgs& a, int bg, int g, float
     const uint16_t* q = a.q_cat + (size_t)bg * a.hd;
     const uint16_t* w = a.wq_t + (size_t)g * a.hd * a.r;
     if (a.r == 32) {
-        // thread -> (feature stride BLOCK/4, j slice of 8): one 16-byte load covers 8 consecutive j of one feature
+        // thread -> (feature stride BLOCK/4, j slice of 8): one 16-byte load covers 8 consecutive j of one feature.
+        // Up to kMaxHd features the loads of all iterations are issued before the first multiply (one memory round
+        // trip instead of one per feature row).
+        constexpr int kIter = kMaxHd / (BLOCK / 4);
         const int js = tid & 3;
         float acc[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-        for (int f = tid >> 2; f < a.hd; f += BLOCK / 4) {
-            const float qf = bf16_to_f32(q[f]);
-            const uint4 wv = *reinterpret_cast<const uint4*>(w + (size_t)f * 32 + js * 8);
-            acc[0] += qf * bf16_lo(wv.x); acc[1] += qf * bf16_hi(wv.x);
-            acc[2] += qf * bf16_lo(wv.y); acc[3] += qf * bf16_hi(wv.y);
-            acc[4] += qf * bf16_lo(wv.z); acc[5] += qf * bf16_hi(wv.z);
-            acc[6] += qf * bf16_lo(wv.w); acc[7] += qf * bf16_hi(wv.w);
+        if (a.hd <= kMaxHd) {
+            uint4 wv[kIter];
+            float qf[kIter];
+#pragma unroll
+            for (int it = 0; it < kIter; ++it) {
+                const int f = (tid >> 2) + it * (BLOCK / 4);
+                wv[it] = make_uint4(0, 0, 0, 0);
+                qf[it] = 0.0f;
+                if (f < a.hd) {
+                    wv[it] = *reinterpret_cast<const uint4*>(w + (size_t)f * 32 + js * 8);
+                    qf[it] = bf16_to_f32(q[f]);
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < kIter; ++it) {
+                acc[0] += qf[it] * bf16_lo(wv[it].x); acc[1] += qf[it] * bf16_hi(wv[it].x);
+                acc[2] += qf[it] * bf16_lo(wv[it].y); acc[3] += qf[it] * bf16_hi(wv[it].y);
+                acc[4] += qf[it] * bf16_lo(wv[it].z); acc[5] += qf[it] * bf16_hi(wv[it].z);
+                acc[6] += qf[it] * bf16_lo(wv[it].w); acc[7] += qf[it] * bf16_hi(wv[it].w);
+            }
+        } else {
+            for (int f = tid >> 2; f < a.hd; f += BLOCK / 4) {
+                const float qv = bf16_to_f32(q[f]);
+                const uint4 wl = *reinterpret_cast<const uint4*>(w + (size_t)f * 32 + js * 8);
+                acc[0] += qv * bf16_lo(wl.x); acc[1] += qv * bf16_hi(wl.x);
+                acc[2] += qv * bf16_lo(wl.y); acc[3] += qv * bf16_hi(wl.y);
+                acc[4] += qv * bf16_lo(wl.z); acc[5] += qv * bf16_hi(wl.z);
+                acc[6] += qv * bf16_lo(wl.w); acc[7] += qv * bf16_hi(wl.w);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -86,11 +112,28 @@ __device__ __forceinline__ void build_u(const ScoreArgs& a, int bg, int g, float
     }
 }
 
-// z column of the newest key: zT[bg, j, write_col] = bf16_rne(wk[g, j, :] . k_new[bg, :]); 8 lanes per j.
+// z column of the newest key: zT[bg, j, write_col] = bf16_rne(wk[g, j, :] . k_new[bg, :]); 8 lanes per j. For d = 128
+// and 16-byte aligned rows each lane reads its 16 elements of wk and k_new with four 16-byte loads.
 template <int BLOCK>
 __device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
     const int tid = threadIdx.x;
     const uint16_t* kn = a.k_new + (size_t)bg * a.d;
+    if (a.d == 128 && a.r <= BLOCK / 8 && ((reinterpret_cast<uintptr_t>(a.wk) | reinterpret_cast<uintptr_t>(kn)) & 15) == 0) {
+        const int j = tid >> 3, e0 = (tid & 7) * 16;
+        float s = 0.0f;
+        if (j < a.r) {
+            const uint16_t* wr = a.wk + ((size_t)g * a.r + j) * 128 + e0;
+            const uint4 w0 = *reinterpret_cast<const uint4*>(wr), w1 = *reinterpret_cast<const uint4*>(wr + 8);
+            const uint4 k0 = *reinterpret_cast<const uint4*>(kn + e0), k1 = *reinterpret_cast<const uint4*>(kn + e0 + 8);
+            s = dot2_bf16(w0.x, k0.x, s); s = dot2_bf16(w0.y, k0.y, s);
+            s = dot2_bf16(w0.z, k0.z, s); s = dot2_bf16(w0.w, k0.w, s);
+            s = dot2_bf16(w1.x, k1.x, s); s = dot2_bf16(w1.y, k1.y, s);
+            s = dot2_bf16(w1.z, k1.z, s); s = dot2_bf16(w1.w, k1.w, s);
+        }
+        s = sum8(s);
+        if ((tid & 7) == 0 && j < a.r) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = f32_to_bf16_rne(s);
+        return;
+    }
     for (int j0 = 0; j0 < a.r; j0 += BLOCK / 8) {
         const int j = j0 + (tid >> 3);
         float s = 0.0f;

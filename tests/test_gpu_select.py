@@ -108,7 +108,8 @@ def test_select_rows_matches_oracle(gpu, legal, k0, order):
 
 @pytest.mark.parametrize("B,C,L,order,tiled", [(1, 2048 + 64, 2048, "position", True), (4, 32768, 32768, "score", True),
                                                (2, 70000, 70000, "position", True), (3, 1000, 777, "score", True),
-                                               (2, 32768, 32768, "position", False)])
+                                               (2, 32768, 32768, "position", False),
+                                               (2, 140000, 140000, "position", True)])
 def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order, tiled):
     """score_grouped(state=) + select_rows(state=) gives exactly the rows of the self-contained select, leaves the
     state zeroed, and stays exact over repeated calls on fresh data (a stale histogram would break it)."""
@@ -171,14 +172,16 @@ def specials(rng, shape):
 
 @pytest.mark.parametrize("M,k,gen", [(1, 1, "normal"), (3, 2, "normal"), (1000, 31, "normal"), (1024, 1024, "normal"),
                                      (1025, 32, "normal"), (4096, 128, "normal"), (4097, 129, "normal"),
-                                     (8191, 4000, "normal"), (32704, 1024, "normal"), (262145, 8192, "normal"), (70000, 2187, "normal"),
+                                     (8191, 4000, "normal"), (32704, 1024, "normal"), (32768, 1024, "normal"),
+                                     (32769, 1025, "normal"), (70000, 2187, "ties"), (131072, 4096, "normal"),
+                                     (262145, 8192, "normal"), (70000, 2187, "normal"),
                                      (3000, 100, "ties"), (32704, 1024, "ties"), (20000, 600, "specials"),
                                      (32704, 32704, "normal"), (5000, 4999, "ties")])
 def test_tiled_select_matches_the_oracle(gpu, M, k, gen):
     """Tiled select (4096-key tiles classified, one workgroup per row resolves) vs the oracle: plain, ties at the
-    threshold (taken in index order), more than 4096 candidates sharing the threshold's first digit
-    (single-workgroup fallback), NaN / +-0 / +-inf, k = M, a row too long for the tiled path (262144 < M); the state
-    is left zeroed and a second call on other data is exact too."""
+    threshold (taken in index order), more than 4096 candidates sharing the threshold's first digit (streaming
+    fallback), NaN / +-0 / +-inf, k = M, long rows, a row too long for the tiled path (262144 < M); the state is left
+    zeroed and a second call on other data is exact too."""
     rng = np.random.default_rng(M + k)
     B, G = 2, 3
     lo = 5
@@ -203,7 +206,7 @@ def test_tiled_select_matches_the_oracle(gpu, M, k, gen):
         assert np.array_equal(rows.cpu().numpy(), want), f"rep {rep}"
         off = (np.arange(B * G) * C).reshape(B, G, 1)
         assert np.array_equal(flat.cpu().numpy().reshape(B, G, -1), want + off)
-        assert int(state.abs().sum()) == 0, "the tiled select must leave the state zeroed"
+        assert int(state.abs().sum()) == 0, "the select must leave the state zeroed"
 
 
 def test_validation(gpu):
