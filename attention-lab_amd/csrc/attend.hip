@@ -12,7 +12,7 @@
 // bf16 dot2 (v_dot2_f32_bf16, fp32 accumulate) finished by a 3-step DPP sum over the 8 lanes; every head of the group
 // reuses the same K and V registers (GQA sharing). Online softmax runs in the log2 domain with a lazy rescale: the
 // running max is raised only when a block max exceeds it by more than 2^8, so the 16*h accumulator rescale is rare.
-// Slots are merged with DPP (lane ^ 8) and v_permlane16/32_swap (lane ^ 16, ^ 32), then the 4 waves through LDS.
+// Slot pairs are merged with DPP (lane ^ 8), then the remaining 16 slots through LDS by (head, dim) columns.
 // With P > 1 partitions every block writes its (m, l, acc) partial and a
 // second small kernel merges them; the kernel boundary is what makes the partials of other XCDs' L2s visible, which
 // is far cheaper on this part than a device-scope fence per block.
@@ -25,6 +25,7 @@ constexpr int kAttThreads = 256;
 constexpr int kSlots = kAttThreads / 8;  // positions in flight per block per step
 constexpr float kLazyRescale = 8.0f;     // log2-domain slack of the running max
 constexpr int kStages = 4;               // K/V groups in flight per wave (LDS stages)
+constexpr int kMergeSlots = 16;          // slots left after the in-register pair merge (4 per wave)
 
 struct AttendArgs {
     const uint16_t* K;
@@ -56,42 +57,6 @@ __device__ __forceinline__ void store_out(const AttendArgs& a, size_t idx, float
     else reinterpret_cast<float*>(a.out)[idx] = v;
 }
 
-// Exchange with lane ^ 16 (SWAP16) or lane ^ 32 and merge, one head at a time: v_permlane16/32_swap hand every lane
-// of a pair both values, lower lane first, so both lanes compute the same merge from the same operands in the same
-// order and end with bit-identical state.
-template <int H, bool SWAP16>
-__device__ __forceinline__ void merge_across(float (&m)[H], float (&l)[H], float (&acc)[H][16]) {
-    auto swap = [](float x, float& lo, float& hi) {
-        const uint32_t u = __float_as_uint(x);
-        if constexpr (SWAP16) {
-            const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-            lo = __uint_as_float(r[0]);
-            hi = __uint_as_float(r[1]);
-        } else {
-            const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-            lo = __uint_as_float(r[0]);
-            hi = __uint_as_float(r[1]);
-        }
-    };
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-        float ma, mb, la, lb;
-        swap(m[i], ma, mb);
-        swap(l[i], la, lb);
-        const float mn = fmaxf(ma, mb);
-        const float w1 = (ma == -INFINITY) ? 0.0f : fast_exp2(ma - mn);
-        const float w2 = (mb == -INFINITY) ? 0.0f : fast_exp2(mb - mn);
-        m[i] = mn;
-        l[i] = w1 * la + w2 * lb;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            float xa, xb;
-            swap(acc[i][e], xa, xb);
-            acc[i][e] = w1 * xa + w2 * xb;
-        }
-    }
-}
-
 // s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding. Loads complete in issue order, so
 // this is how the kernel knows that the LDS copies of an older stage have landed (the compiler does not track the LDS
 // writes of global_load_lds).
@@ -111,8 +76,8 @@ __device__ __forceinline__ void read_stage(const uint4* st_lane, u32x4_t& k0, u3
         "ds_read_b128 %2, %4 offset:2048\n"
         "ds_read_b128 %3, %4 offset:3072\n"
         "s_waitcnt lgkmcnt(0)"
-        : "=v"(k0), "=v"(k1), "=v"(v0), "=v"(v1)
-        : "v"(addr)
+        : "=&v"(k0), "=&v"(k1), "=&v"(v0), "=&v"(v1)   // early clobber: no output may share the address register,
+        : "v"(addr)                                      // which later reads of the block still use
         : "memory");
 }
 
@@ -121,8 +86,8 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     constexpr int kChunk = 1024;   // row-list entries whose positions are staged in LDS at a time
     __shared__ __attribute__((aligned(16))) uint4 stage[4][D][4][64];   // [wave][stage][K lo, K hi, V lo, V hi][lane]
     __shared__ int idx_sh[DENSE ? 1 : kChunk];
-    __shared__ float red_ml[4][H][2];
-    static_assert(sizeof(float) * 4 * H * kHeadDim <= sizeof(uint4) * 4 * D * 4 * 64, "wave merge buffer");
+    __shared__ float red_ml[kMergeSlots][H][2];
+    static_assert(sizeof(float) * kMergeSlots * H * kHeadDim <= sizeof(uint4) * 4 * D * 4 * 64, "slot merge buffer");
     float (*red_acc)[H][kHeadDim] = reinterpret_cast<float (*)[H][kHeadDim]>(&stage[0][0][0][0]);
     const int bg = blockIdx.x / a.P;
     const int p = blockIdx.x - bg * a.P;
@@ -246,7 +211,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         }
     }
 
-    // merge the 8 slots of the wave (lanes with equal `sub`): xor 8 (DPP row_ror:8), then xor 16 and xor 32
+    // Merge the 32 slots of the block: slots 2s and 2s + 1 (lane ^ 8, DPP row_ror:8) in registers, then the 16
+    // merged slots through LDS, where every thread reduces whole (head, dim) columns. The register-only merge over
+    // lane ^ 16 and lane ^ 32 that this replaces took about 2 us per workgroup on MI355X.
 #pragma unroll
     for (int i = 0; i < H; ++i) {
         float m2 = dpp_f32<0x128>(m[i]), l2 = dpp_f32<0x128>(l[i]);
@@ -255,33 +222,32 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][e] = w1 * acc[i][e] + w2 * dpp_f32<0x128>(acc[i][e]);
     }
-    merge_across<H, true>(m, l, acc);
-    merge_across<H, false>(m, l, acc);
-    __syncthreads();   // the wave merge buffer overlays the stages of every wave
-    if (lane < 8) {
+    __syncthreads();   // the merge buffer overlays the stages of every wave
+    const int rs = wave * 4 + (lane >> 4);   // merged slot: one per 16-lane row
+    if ((lane & 15) < 8) {
 #pragma unroll
         for (int i = 0; i < H; ++i) {
-            if (lane == 0) {
-                red_ml[wave][i][0] = m[i];
-                red_ml[wave][i][1] = l[i];
+            if (sub == 0) {
+                red_ml[rs][i][0] = m[i];
+                red_ml[rs][i][1] = l[i];
             }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                red_acc[wave][i][8 * sub + e] = acc[i][e];
-                red_acc[wave][i][64 + 8 * sub + e] = acc[i][8 + e];
-            }
+            float4* r0 = reinterpret_cast<float4*>(&red_acc[rs][i][8 * sub]);
+            float4* r1 = reinterpret_cast<float4*>(&red_acc[rs][i][64 + 8 * sub]);
+            r0[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+            r0[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+            r1[0] = make_float4(acc[i][8], acc[i][9], acc[i][10], acc[i][11]);
+            r1[1] = make_float4(acc[i][12], acc[i][13], acc[i][14], acc[i][15]);
         }
     }
     __syncthreads();
-    // merge the 4 waves: thread -> (head, dim) pairs
     for (int idx = tid; idx < h * kHeadDim; idx += kAttThreads) {
         const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
         float ms = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) ms = fmaxf(ms, red_ml[w][i][0]);
+        for (int w = 0; w < kMergeSlots; ++w) ms = fmaxf(ms, red_ml[w][i][0]);
         float ls = 0.0f, as = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < kMergeSlots; ++w) {
             const float mw = red_ml[w][i][0];
             const float ww = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - ms);
             ls += ww * red_ml[w][i][1];
