@@ -351,6 +351,85 @@ __global__ __launch_bounds__(256) void score_prologue(ScoreArgs a) {
     if (a.k_new) write_z<256>(a, bg, g);
 }
 
+// The prologue for r = 32, d = 128, q_cat features hd <= 512 and 16-byte aligned operands, spread over four workgroups
+// per (b, g): workgroup `part` computes u[j] and the z entry for j in [8 part, 8 part + 8). One workgroup per (b, g)
+// has to stream 41 KB of weights and queries through a single CU, whose outstanding-miss budget, not bandwidth,
+// bounds it; a quarter of the weights per CU halves the kernel time.
+__global__ __launch_bounds__(256) void score_prologue_split(ScoreArgs a) {
+    __shared__ float red[4][8];
+    __shared__ float zred[8];
+    const int bg = blockIdx.x >> 2, part = blockIdx.x & 3;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // u: thread -> features tid and tid + 256 (when below hd), 8 j of this part per feature (one 16-byte load)
+    const uint16_t* q = a.q_cat + (size_t)bg * a.hd;
+    const uint16_t* w = a.wq_t + (size_t)g * a.hd * 32 + part * 8;
+    uint4 wv[2];
+    float qf[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int f = tid + it * 256;
+        wv[it] = make_uint4(0, 0, 0, 0);
+        qf[it] = 0.0f;
+        if (f < a.hd) {
+            wv[it] = *reinterpret_cast<const uint4*>(w + (size_t)f * 32);
+            qf[it] = bf16_to_f32(q[f]);
+        }
+    }
+    // z: thread -> (j = 8 part + tid / 32, elements 4 (tid % 32) .. + 4)
+    float zs = 0.0f;
+    const int zj = part * 8 + (tid >> 5), ze = (tid & 31) * 4;
+    if (a.k_new) {
+        const uint16_t* wr = a.wk + ((size_t)g * 32 + zj) * 128 + ze;
+        const uint16_t* kn = a.k_new + (size_t)bg * 128 + ze;
+        const uint2 w2 = *reinterpret_cast<const uint2*>(wr), k2 = *reinterpret_cast<const uint2*>(kn);
+        zs = dot2_bf16(w2.x, k2.x, zs);
+        zs = dot2_bf16(w2.y, k2.y, zs);
+    }
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        acc[0] += qf[it] * bf16_lo(wv[it].x); acc[1] += qf[it] * bf16_hi(wv[it].x);
+        acc[2] += qf[it] * bf16_lo(wv[it].y); acc[3] += qf[it] * bf16_hi(wv[it].y);
+        acc[4] += qf[it] * bf16_lo(wv[it].z); acc[5] += qf[it] * bf16_hi(wv[it].z);
+        acc[6] += qf[it] * bf16_lo(wv[it].w); acc[7] += qf[it] * bf16_hi(wv[it].w);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float v = acc[i];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) v += shfl_xor_f32(v, o);
+        acc[i] = v;
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) red[wave][i] = acc[i];
+    }
+    if (a.k_new) {
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) zs += shfl_xor_f32(zs, o);
+        if ((tid & 31) == 0) zred[tid >> 5] = zs;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        const float u = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+        a.u_out[(size_t)bg * 32 + part * 8 + tid] = u;
+        if (a.k_new)
+            a.zT[((size_t)bg * 32 + part * 8 + tid) * a.C + a.write_col] = f32_to_bf16_rne(zred[tid]);
+    }
+}
+
+// Launch the prologue (u into a.u_out, and the z column when a.k_new is set) over B*G rows.
+static void launch_prologue(const ScoreArgs& a, int BG, hipStream_t s) {
+    const bool split = a.r == 32 && a.hd <= 512 && a.u_out != nullptr && (a.k_new == nullptr || a.d == 128) &&
+                       ((reinterpret_cast<uintptr_t>(a.wq_t) | reinterpret_cast<uintptr_t>(a.wk) |
+                         reinterpret_cast<uintptr_t>(a.k_new)) & 15) == 0;
+    if (split) hipLaunchKernelGGL(score_prologue_split, dim3(BG * 4), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(score_prologue, dim3(BG), dim3(256), 0, s, a);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Lightning mode. Block = 256 threads = 64 positions (4 lanes x 16 bytes each); q and w are staged in LDS.
 // ---------------------------------------------------------------------------------------------------------------
@@ -517,13 +596,13 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
     const int BG = B * G;
     if (M == 0) {
         if (!k_new && !u_out) return ATTNLAB_OK;
-        hipLaunchKernelGGL(score_prologue, dim3(BG), dim3(256), 0, s, a);
+        launch_prologue(a, BG, s);
         return check_launch("score_prologue");
     }
     if (u_in == nullptr && u_out != nullptr) {
         // two launches: u (and the z column) once per (b, g), then a scan that only stages u; the per-block u of the
         // single-launch form costs ~20% of the scan time at B=16, L=32K
-        hipLaunchKernelGGL(score_prologue, dim3(BG), dim3(256), 0, s, a);
+        launch_prologue(a, BG, s);
         const int rc = check_launch("score_prologue");
         if (rc) return rc;
         a.u_in = u_out;
@@ -554,7 +633,7 @@ extern "C" int attnlab_score_prologue(uint16_t* zT, const uint16_t* k_new, const
     if (k_new) ATTNLAB_REQUIRE(zT && wk && 0 <= write_col && write_col < C, "write_col=%d outside [0, %d)", write_col, C);
     if (r == 32) ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(wq_t) % 16 == 0, "wq_t must be 16-byte aligned");
     ScoreArgs a{zT, k_new, wk, q_cat, wq_t, nullptr, u_out, nullptr, 0, G, r, C, d, hd, 0, 0, write_col, 1};
-    hipLaunchKernelGGL(score_prologue, dim3(B * G), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    launch_prologue(a, B * G, reinterpret_cast<hipStream_t>(stream));
     return check_launch("score_prologue");
 }
 
