@@ -17,7 +17,7 @@ LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 3
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
-# score key), then reserved words, padded to 256 bytes (ATTNLAB_SELECT_STATE_WORDS)
+# score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
 SELECT_STATE_WORDS = 2112
 
 ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2

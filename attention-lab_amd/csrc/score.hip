@@ -150,11 +150,25 @@ __device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
 // histogram with one device atomic per non-empty bin. Called by every thread of the block.
 template <int BLOCK>
 __device__ __forceinline__ void flush_histogram(uint32_t* hsh, uint32_t* ghist, int bg) {
+    static_assert(BLOCK >= kSuperBins, "one thread per super-bin");
     __syncthreads();
     uint32_t* row = ghist + (size_t)bg * kSelectStateWords;
+    // bins: thread t -> t, t + BLOCK, ...: the lanes of one atomic instruction hit consecutive words (two lines)
     for (int b = threadIdx.x; b < kHistBins; b += BLOCK) {
         const uint32_t c = hsh[b];
         if (c) atomicAdd(row + b, c);
+    }
+    // super-bins: lane s of the first wave sums bins [32 s, 32 s + 32), starting at a lane-dependent chunk so the
+    // lanes spread over the LDS banks
+    if (threadIdx.x < kSuperBins) {
+        const int sb = threadIdx.x;
+        uint32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hsh + 32 * sb + 4 * ((sb + j) & 7));
+            sum += v.x + v.y + v.z + v.w;
+        }
+        if (sum) atomicAdd(row + kHistBins + sb, sum);
     }
 }
 
@@ -173,7 +187,7 @@ template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void score_scan_vec(ScoreArgs a) {
     __shared__ float u_sh[32];
     __shared__ float red[(BLOCK / 64) * 32];
-    __shared__ uint32_t hsh[kHistBins];
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     const int bg = blockIdx.x / a.tiles;
     const int tile = blockIdx.x - bg * a.tiles;
     const int g = bg % a.G;
@@ -236,7 +250,7 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
     static_assert(BLOCK == 256, "four waves of eight table rows");
     constexpr int kCols = 512;
     __shared__ float u_sh[32];
-    __shared__ uint32_t hsh[kHistBins];
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     __shared__ __attribute__((aligned(16))) float part[4][kCols];
     const int bg = blockIdx.x / a.tiles;
     const int tile = blockIdx.x - bg * a.tiles;
@@ -302,7 +316,7 @@ template <int BLOCK>
 __global__ __launch_bounds__(BLOCK) void score_scan_scalar(ScoreArgs a) {
     __shared__ float u_sh[32];
     __shared__ float red[(BLOCK / 64) * 32];
-    __shared__ uint32_t hsh[kHistBins];
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     const int bg = blockIdx.x / a.tiles;
     const int tile = blockIdx.x - bg * a.tiles;
     const int g = bg % a.G;

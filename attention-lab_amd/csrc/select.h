@@ -10,8 +10,11 @@ constexpr int kHistBits = 11;                 // first digit: sign, exponent and
 constexpr int kHistBins = 1 << kHistBits;
 constexpr int kHistShift = 32 - kHistBits;
 // Per-row select state shared by the score and select kernels: the first-digit histogram (kHistBins words), then
-// reserved words, padded to 256 bytes. Zero before the first call; the select leaves it zero.
-constexpr int kSelectStateWords = 2112;
+// kSuperBins counts of 32 consecutive bins each (so the threshold's first digit is found from 64 + 32 words instead of
+// 2048). Zero before the first call; the select leaves it zero.
+constexpr int kSuperBins = kHistBins / 32;
+constexpr int kSelectStateWords = kHistBins + kSuperBins;
+static_assert(kSelectStateWords == 2112, "ABI: ATTNLAB_SELECT_STATE_WORDS");
 
 // Order-preserving key: larger float -> larger key; -0 -> +0; NaN -> 0 (below -inf, whose key is 0x007fffff).
 __device__ __forceinline__ uint32_t score_key(float f) {

@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
         }
     }
     if (ghist)  // leave the first-digit histogram zeroed for the next score/select pair
-        for (int i = tid; i < kHistBins; i += kSelThreads) ghist[i] = 0u;
+        for (int i = tid; i < kSelectStateWords; i += kSelThreads) ghist[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);
 }
@@ -345,7 +345,7 @@ __device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared&
         }
     }
     if (ghist)
-        for (int i = tid; i < kHistBins; i += kSelThreads) ghist[i] = 0u;
+        for (int i = tid; i < kSelectStateWords; i += kSelThreads) ghist[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);
 }
@@ -368,8 +368,8 @@ static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // Tiled select (position order, first-digit histogram given), two launches:
-//   A select_classify  (rows x tiles of 4096 keys, 256 threads): the threshold's first digit b1 from the row
-//                      histogram; every key of the tile is classified as "above" (first digit > b1: selected for sure)
+//   A select_classify  (rows x tiles of 4096 keys, 256 threads): the threshold's first digit b1 from the row's
+//                      super-bins and bins; every key of the tile is classified as "above" (first digit > b1: selected for sure)
 //                      or "candidate" (first digit == b1), written as two bitmaps of the row (one bit per key).
 //   B select_resolve   (one 1024-thread workgroup per row): compacts the candidate bitmap into an index-ordered list,
 //                      gathers the candidates' scores, finds the threshold among them with the remaining two radix
@@ -397,24 +397,24 @@ __host__ __device__ inline int64_t tiled_scratch_bytes(int R, int M) {
     return (int64_t)R * 2 * 4 * (((int64_t)M + 31) / 32);
 }
 
-// b1 = first digit of the k-th largest key, from the row histogram; thread t holds the counts c[0..BPT) of bins
-// (THREADS - 1 - t) * BPT + i, so thread 0 owns the highest bins. Writes *out when the histogram holds at least k keys
-// (else *out keeps what the caller put there). Ends synchronised.
-template <int THREADS, int BPT>
-__device__ __forceinline__ void first_digit(const uint32_t (&c)[BPT], uint32_t k, uint32_t (*wave_tot)[2],
-                                            uint32_t* out) {
-    const int rt = THREADS - 1 - (int)threadIdx.x;
-    uint32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < BPT; ++i) sum += c[i];
-    uint32_t above, unused, tot, unused_tot;
-    block_scan2<THREADS>(sum, 0u, above, unused, tot, unused_tot, wave_tot);
-#pragma unroll
-    for (int i = BPT - 1; i >= 0; --i) {
-        if (above < k && above + c[i] >= k) *out = (uint32_t)(rt * BPT + i);
-        above += c[i];
-    }
-    __syncthreads();
+// b1 = first digit of the k-th largest key, from the row's select state: one wave scans the 64 super-bins (lane 0 =
+// the highest), picks the one holding the k-th key, then scans its 32 bins. Two small loads and two DPP scans, no LDS
+// and no barrier, so every wave can run it on its own. Returns 0 when the state holds fewer than k keys.
+__device__ __forceinline__ uint32_t first_digit_2level(const uint32_t* st, uint32_t k) {
+    static_assert(kSuperBins == 64, "one super-bin per lane");
+    const int lane = threadIdx.x & 63;
+    const uint32_t v = st[kHistBins + (kSuperBins - 1 - lane)];
+    const uint32_t inc = wave_incl_scan(v);
+    const uint64_t m = __ballot(inc >= k);
+    if (m == 0) return 0u;
+    const int l0 = __ffsll((unsigned long long)m) - 1;
+    const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)(inc - v), l0);
+    const int sb = kSuperBins - 1 - l0;
+    const uint32_t c = lane < 32 ? st[32 * sb + (31 - lane)] : 0u;
+    const uint32_t inc2 = wave_incl_scan(c) + above;
+    const uint64_t m2 = __ballot(lane < 32 && inc2 >= k);
+    if (m2 == 0) return (uint32_t)(32 * sb);
+    return (uint32_t)(32 * sb + 31 - (__ffsll((unsigned long long)m2) - 1));
 }
 
 // This thread's 16 scores of the tile as raw floats; positions at or past M are not read.
@@ -437,11 +437,8 @@ __device__ __forceinline__ int load_tile_scores(const float* s, int i0, int M, f
 }
 
 __global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, TiledArgs t) {
-    __shared__ uint32_t wave_tot[kTileThreads / 64][2];
-    __shared__ uint32_t sh_b1;
-    constexpr int kBPT = kHistBins / kTileThreads;   // 8 histogram bins per thread
-    // the tiles of one row go to one XCD (workgroups are dealt to the 8 XCDs round robin), so the row's histogram
-    // is fetched into that XCD's L2 once
+    // the tiles of one row go to one XCD (workgroups are dealt to the 8 XCDs round robin), so the row's super-bins
+    // and bins are fetched into that XCD's L2 once
     int lin = blockIdx.x;
     if ((gridDim.x & 7) == 0) lin = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
     const int row = lin / t.T, tile = lin - row * t.T;
@@ -450,13 +447,7 @@ __global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, Ti
     const int i0 = tile * kTileKeys + tid * kTileKPT;
     float v[kTileKPT];
     const int nvalid = load_tile_scores(s, i0, a.M, v);
-    const int rt = kTileThreads - 1 - tid;
-    const uint4* gh = reinterpret_cast<const uint4*>(a.hist + (size_t)row * kSelectStateWords + rt * kBPT);
-    const uint4 h0 = gh[0], h1 = gh[1];
-    if (tid == 0) sh_b1 = 0u;
-    const uint32_t c[kBPT] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-    first_digit<kTileThreads, kBPT>(c, (uint32_t)a.k, wave_tot, &sh_b1);
-    const uint32_t b1 = sh_b1;
+    const uint32_t b1 = first_digit_2level(a.hist + (size_t)row * kSelectStateWords, (uint32_t)a.k);
     uint32_t abits = 0, cbits = 0;
 #pragma unroll
     for (int i = 0; i < kTileKPT; ++i) {
@@ -601,7 +592,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
         if (flat) flat[s_out] = base + p;
     }
     uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
-    for (int i = tid; i < kHistBins; i += kSelThreads) st[i] = 0u;
+    for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
 }
 
 static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s) {

@@ -40,7 +40,7 @@ extern "C" {
 #define ATTNLAB_DT_F32 2
 
 /* Words per row of the select state shared by attnlab_score_grouped and attnlab_select_rows: the first-digit
- * histogram (2048 bins), then reserved words, padded to 256 bytes. */
+ * histogram (2048 bins), then 64 super-bin counts (sums of 32 consecutive bins). */
 #define ATTNLAB_SELECT_STATE_WORDS 2112
 
 /* ABI version; bumped on any signature change. */

@@ -144,7 +144,8 @@ def score_keys(s):
 
 
 def state_for(s):
-    """Select state [B, G, 2112] whose histogram is that of the scores' first 11-bit digit (counter word zero)."""
+    """Select state [B, G, 2112] of the scores: the histogram of their first 11-bit digit, then its 64 sums of 32
+    consecutive bins (what the score kernel leaves for the select)."""
     from attention_lab import _native as nat
     B, G, M = s.shape
     st = np.zeros((B, G, nat.SELECT_STATE_WORDS), dtype=np.int64)
@@ -152,6 +153,7 @@ def state_for(s):
     for b in range(B):
         for g in range(G):
             st[b, g, :2048] = np.bincount(d[b, g], minlength=2048)
+    st[..., 2048:2112] = st[..., :2048].reshape(B, G, 64, 32).sum(-1)
     return torch.from_numpy(st.astype(np.int32))
 
 
