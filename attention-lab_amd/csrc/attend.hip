@@ -6,9 +6,10 @@
 //
 // Layout per workgroup (256 threads = 4 waves) of one (b, g, partition): 8 lanes share a position; lane `sub` owns
 // dims [8*sub, 8*sub+8) and [64+8*sub, 64+8*sub+8), so one 16-byte load per lane and half-row covers 128 contiguous
-// bytes (one cache line) and a wave reads 8 positions per load instruction. The 32 position slots of the block walk
-// the partition with stride 32, R positions per iteration, software-pipelined over two register sets: the row
-// indices of iteration i+2 and the K/V rows of iteration i+1 are in flight while iteration i is computed. q . k is a
+// bytes (one cache line) and a wave reads 8 positions per load instruction. Each wave walks its groups of 8 positions
+// through kStages rotating register stages: while one group is computed, the K/V rows of the next kStages - 1 groups
+// are in flight. (Staging the rows through LDS with global_load_lds instead caps a CU at about 10 GB/s on MI355X, less
+// than half of what plain 16-byte loads reach on the same random rows.) q . k is a
 // bf16 dot2 (v_dot2_f32_bf16, fp32 accumulate) finished by a 3-step DPP sum over the 8 lanes; every head of the group
 // reuses the same K and V registers (GQA sharing). Online softmax runs in the log2 domain with a lazy rescale: the
 // running max is raised only when a block max exceeds it by more than 2^8, so the 16*h accumulator rescale is rare.
@@ -22,10 +23,10 @@ namespace attnlab {
 
 constexpr int kHeadDim = 128;
 constexpr int kAttThreads = 256;
-constexpr int kSlots = kAttThreads / 8;  // positions in flight per block per step
+constexpr int kAttWaves = kAttThreads / 64;
 constexpr float kLazyRescale = 8.0f;     // log2-domain slack of the running max
-constexpr int kStages = 4;               // K/V groups in flight per wave (LDS stages)
-constexpr int kMergeSlots = 16;          // slots left after the in-register pair merge (4 per wave)
+constexpr int kStages = 4;               // K/V groups per wave in registers: D - 1 in flight while one is computed
+constexpr int kMergeSlots = 4 * kAttWaves;  // slots left after the in-register pair merge (4 per wave)
 
 struct AttendArgs {
     const uint16_t* K;
@@ -57,38 +58,18 @@ __device__ __forceinline__ void store_out(const AttendArgs& a, size_t idx, float
     else reinterpret_cast<float*>(a.out)[idx] = v;
 }
 
-// s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still outstanding. Loads complete in issue order, so
-// this is how the kernel knows that the LDS copies of an older stage have landed (the compiler does not track the LDS
-// writes of global_load_lds).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// The four 16-byte LDS words of this lane in a stage (K lo, K hi, V lo, V hi at 1 KiB spacing), read in inline
-// assembly: a plain LDS read of memory that global_load_lds also writes makes the compiler wait for every outstanding
-// load (vmcnt(0)), which would serialise the pipeline; the caller's wait_vmcnt is what orders these reads.
-__device__ __forceinline__ void read_stage(const uint4* st_lane, u32x4_t& k0, u32x4_t& k1, u32x4_t& v0, u32x4_t& v1) {
-    const uint32_t addr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint4*)st_lane;
-    asm volatile(
-        "ds_read_b128 %0, %4\n"
-        "ds_read_b128 %1, %4 offset:1024\n"
-        "ds_read_b128 %2, %4 offset:2048\n"
-        "ds_read_b128 %3, %4 offset:3072\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k0), "=&v"(k1), "=&v"(v0), "=&v"(v1)   // early clobber: no output may share the address register,
-        : "v"(addr)                                      // which later reads of the block still use
-        : "memory");
-}
+// One pipeline stage of a wave: this lane's 16-byte words of the K and V rows of its slot's position.
+struct KVStage {
+    u32x4_t k0, k1, v0, v1;
+    bool ok;   // the entry exists and its position is inside [0, C)
+};
 
 template <int H, int D, bool DENSE>
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     constexpr int kChunk = 1024;   // row-list entries whose positions are staged in LDS at a time
-    __shared__ __attribute__((aligned(16))) uint4 stage[4][D][4][64];   // [wave][stage][K lo, K hi, V lo, V hi][lane]
     __shared__ int idx_sh[DENSE ? 1 : kChunk];
     __shared__ float red_ml[kMergeSlots][H][2];
-    static_assert(sizeof(float) * kMergeSlots * H * kHeadDim <= sizeof(uint4) * 4 * D * 4 * 64, "slot merge buffer");
-    float (*red_acc)[H][kHeadDim] = reinterpret_cast<float (*)[H][kHeadDim]>(&stage[0][0][0][0]);
+    __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
     const int bg = blockIdx.x / a.P;
     const int p = blockIdx.x - bg * a.P;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -134,46 +115,40 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = rl[c0 + i];
             __syncthreads();
         }
-        // The chunk's entries form groups of 8 (one per slot of a wave); wave w takes groups w, w + 4, ...
+        // The chunk's entries form groups of 8 (one per slot of a wave); wave w takes groups w, w + kAttWaves, ...
         const int ng = (clen + 7) / 8;
-        const int my_ng = ng > wave ? (ng - wave + 3) / 4 : 0;
-        // Stage j of this wave <- K/V rows of its j-th group: four 16-byte loads per lane straight into LDS, lane l's
-        // bytes at lane offset 16 l. Entries past the chunk or outside [0, C) load row 0 (in bounds) and are masked
-        // in compute, so every group issues exactly four loads.
-        auto issue = [&](int j) {
-            const int e = (wave + 4 * j) * 8 + slot;
-            int pos = 0;
-            if (e < clen) {
-                pos = DENSE ? c0 + e : idx_sh[e];
-                if (!DENSE && (unsigned)pos >= (unsigned)a.C) pos = 0;
-            }
+        const int my_ng = ng > wave ? (ng - wave + kAttWaves - 1) / kAttWaves : 0;
+        // Group j of this wave -> a register stage: four 16-byte loads per lane (K lo, K hi, V lo, V hi of its slot's
+        // row). Entries past the chunk (also whole groups past the wave's last) or outside [0, C) load row 0, which is
+        // in bounds, and are masked in compute. No branch: every path issues the same loads, so the compiler's wait
+        // before a stage is used counts exactly the 4 (D - 1) loads issued after it.
+        auto issue = [&](int j, KVStage& s) {
+            const int e = (wave + kAttWaves * j) * 8 + slot;
+            int pos = DENSE ? c0 + e : idx_sh[min(e, clen - 1)];
+            const bool ok = e < clen && (DENSE || (unsigned)pos < (unsigned)a.C);
+            pos = ok ? pos : 0;
             const size_t off = (size_t)pos * a.kv_row_stride;
-            uint4* st = &stage[wave][j % D][0][0];
-            __builtin_amdgcn_global_load_lds(Kb + off, st, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Kb + off + 64, st + 64, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Vb + off, st + 128, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Vb + off + 64, st + 192, 16, 0, 0);
+            s.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(Kb + off));
+            s.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(Kb + off + 64));
+            s.v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(Vb + off));
+            s.v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(Vb + off + 64));
+            s.ok = ok;
         };
-        auto compute = [&](int j) {
-            const int e = (wave + 4 * j) * 8 + slot;
-            bool ok = e < clen;
-            if (!DENSE && ok) ok = (unsigned)idx_sh[e] < (unsigned)a.C;
-            u32x4_t k0, k1, v0, v1;
-            read_stage(&stage[wave][j % D][0][lane], k0, k1, v0, v1);
+        auto compute = [&](const KVStage& s) {
             float sc[H];
 #pragma unroll
             for (int i = 0; i < H; ++i) {
                 float d = 0.0f;
-                d = dot2_bf16(qw[i][0], k0.x, d);
-                d = dot2_bf16(qw[i][1], k0.y, d);
-                d = dot2_bf16(qw[i][2], k0.z, d);
-                d = dot2_bf16(qw[i][3], k0.w, d);
-                d = dot2_bf16(qw[i][4], k1.x, d);
-                d = dot2_bf16(qw[i][5], k1.y, d);
-                d = dot2_bf16(qw[i][6], k1.z, d);
-                d = dot2_bf16(qw[i][7], k1.w, d);
+                d = dot2_bf16(qw[i][0], s.k0.x, d);
+                d = dot2_bf16(qw[i][1], s.k0.y, d);
+                d = dot2_bf16(qw[i][2], s.k0.z, d);
+                d = dot2_bf16(qw[i][3], s.k0.w, d);
+                d = dot2_bf16(qw[i][4], s.k1.x, d);
+                d = dot2_bf16(qw[i][5], s.k1.y, d);
+                d = dot2_bf16(qw[i][6], s.k1.z, d);
+                d = dot2_bf16(qw[i][7], s.k1.w, d);
                 d = sum8(d);
-                sc[i] = ok ? d * a.scale_log2 : -INFINITY;
+                sc[i] = s.ok ? d * a.scale_log2 : -INFINITY;
                 if (sc[i] > m[i] + kLazyRescale) {
                     const float al = fast_exp2(m[i] - sc[i]);
                     l[i] *= al;
@@ -183,7 +158,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
                 }
             }
             float vf[16];
-            const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            const uint32_t vw[8] = {s.v0.x, s.v0.y, s.v0.z, s.v0.w, s.v1.x, s.v1.y, s.v1.z, s.v1.w};
 #pragma unroll
             for (int w = 0; w < 8; ++w) {
                 vf[2 * w] = bf16_lo(vw[w]);
@@ -191,23 +166,31 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < H; ++i) {
-                const float pr = ok ? fast_exp2(sc[i] - m[i]) : 0.0f;
+                const float pr = s.ok ? fast_exp2(sc[i] - m[i]) : 0.0f;
                 l[i] += pr;
 #pragma unroll
                 for (int q = 0; q < 16; ++q) acc[i][q] += pr * vf[q];
             }
         };
-        const int pro = min(D - 1, my_ng);
-        for (int j = 0; j < pro; ++j) issue(j);
-        for (int j = 0; j < my_ng; ++j) {
-            if (j + D - 1 < my_ng) {
-                asm volatile("" ::: "memory");   // the stage refilled below was read by compute(j - 1)
-                issue(j + D - 1);
-                wait_vmcnt<4 * (D - 1)>();        // group j's four loads are older than the 4 (D - 1) after them
-            } else {
-                wait_vmcnt<0>();
+        // D register stages rotate: while group j is computed, groups j + 1 .. j + D - 1 are in flight. The main loop
+        // runs whole blocks of D groups, unrolled so that every stage index is a constant (the stages stay in
+        // registers) and with its only exit at the block's end, so the wait before each stage's use stays exact.
+        // The last < D groups are already in flight when it ends; the tail only computes them.
+        if (my_ng > 0) {
+            KVStage st[D];
+#pragma unroll
+            for (int u = 0; u < D - 1; ++u) issue(u, st[u]);
+            int j = 0;
+            for (; j + D <= my_ng; j += D) {
+#pragma unroll
+                for (int u = 0; u < D; ++u) {
+                    issue(j + u + D - 1, st[(u + D - 1) % D]);
+                    compute(st[u]);
+                }
             }
-            compute(j);
+#pragma unroll
+            for (int u = 0; u < D - 1; ++u)
+                if (j + u < my_ng) compute(st[u]);
         }
     }
 
@@ -222,7 +205,6 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][e] = w1 * acc[i][e] + w2 * dpp_f32<0x128>(acc[i][e]);
     }
-    __syncthreads();   // the merge buffer overlays the stages of every wave
     const int rs = wave * 4 + (lane >> 4);   // merged slot: one per 16-lane row
     if ((lane & 15) < 8) {
 #pragma unroll
