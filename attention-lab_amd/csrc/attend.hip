@@ -70,8 +70,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     __shared__ int idx_sh[DENSE ? 1 : kChunk];
     __shared__ float red_ml[kMergeSlots][H][2];
     __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
-    const int bg = blockIdx.x / a.P;
-    const int p = blockIdx.x - bg * a.P;
+    const int lin = xcd_contiguous_block();   // (b, g) on the XCD that wrote its row list
+    const int bg = lin / a.P;
+    const int p = lin - bg * a.P;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int slot = lane >> 3;

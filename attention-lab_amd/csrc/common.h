@@ -86,6 +86,14 @@ __device__ __forceinline__ float shfl_xor_f32(float x, int mask) { return __shfl
 // exp2 on the hardware transcendental unit (v_exp_f32); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroups of a launch are dealt to MI355X's 8 XCDs round robin (workgroup b runs on XCD b % 8), each with its own
+// L2. This renumbers them so that XCD x gets the contiguous logical range [x * n / 8, (x + 1) * n / 8) when the grid
+// size n is a multiple of 8: kernels that split the same rows the same way then touch a row's data from one XCD.
+__device__ __forceinline__ int xcd_contiguous_block() {
+    const int b = blockIdx.x, n = gridDim.x;
+    return (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 }  // namespace attnlab

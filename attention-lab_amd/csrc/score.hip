@@ -252,8 +252,9 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
     __shared__ float u_sh[32];
     __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     __shared__ __attribute__((aligned(16))) float part[4][kCols];
-    const int bg = blockIdx.x / a.tiles;
-    const int tile = blockIdx.x - bg * a.tiles;
+    const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
+    const int bg = lin / a.tiles;
+    const int tile = lin - bg * a.tiles;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lo = a.lo, hi = a.lo + a.M;
     const int cb = (lo & ~7) + tile * kCols;
@@ -372,7 +373,8 @@ __global__ __launch_bounds__(256) void score_prologue(ScoreArgs a) {
 __global__ __launch_bounds__(256) void score_prologue_split(ScoreArgs a) {
     __shared__ float red[4][8];
     __shared__ float zred[8];
-    const int bg = blockIdx.x >> 2, part = blockIdx.x & 3;
+    const int lin = xcd_contiguous_block();   // (b, g) on the XCD that scans its row
+    const int bg = lin >> 2, part = lin & 3;
     const int g = bg % a.G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // u: thread -> features tid and tid + 256 (when below hd), 8 j of this part per feature (one 16-byte load)

@@ -437,10 +437,9 @@ __device__ __forceinline__ int load_tile_scores(const float* s, int i0, int M, f
 }
 
 __global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, TiledArgs t) {
-    // the tiles of one row go to one XCD (workgroups are dealt to the 8 XCDs round robin), so the row's super-bins
-    // and bins are fetched into that XCD's L2 once
-    int lin = blockIdx.x;
-    if ((gridDim.x & 7) == 0) lin = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    // the tiles of one row go to one XCD, the one that scanned the row and resolves it, so the row's select state
+    // and scores are fetched into that XCD's L2 once
+    const int lin = xcd_contiguous_block();
     const int row = lin / t.T, tile = lin - row * t.T;
     const int tid = threadIdx.x;
     const float* s = a.scores + (size_t)row * a.score_stride;
@@ -470,7 +469,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     __shared__ SelectShared sh;                 // sortbuf holds the candidate list (as uint32 indices)
     __shared__ uint32_t hist3[1024];
     __shared__ uint32_t bits[kMaxWords];
-    const int row = blockIdx.x;
+    const int row = xcd_contiguous_block();   // the XCD that classified the row
     const int tid = threadIdx.x;
     const int W = t.W;
     const int wpt = (W + kSelThreads - 1) / kSelThreads;   // <= kMaxWordsPerThread
