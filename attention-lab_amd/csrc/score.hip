@@ -311,6 +311,134 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
     if (a.hist) flush_histogram<BLOCK>(hsh, a.hist, bg);
 }
 
+// The v16 scan with the prologue folded in (r = 32, q_cat features hd <= 512, 16-byte aligned operands): one launch per
+// step instead of two, which saves a kernel boundary (a few microseconds of launch, drain and cache maintenance on
+// MI355X, more than the prologue's own work). Wave w needs u[j] only for its own j in [8w, 8w + 8): it reads those 8
+// weights of every q_cat feature (one 16-byte load per feature, 8 KB per wave, L2-resident) right after its first
+// table loads are in flight, and reduces them in registers (DPP within rows of 16 lanes, then readlane), so u costs no
+// barrier. A workgroup covers NSUB consecutive 512-column sub-tiles, double-buffered (the loads of sub-tile s + 1 are
+// issued before sub-tile s is reduced), which spreads the weight reads and the histogram flush over NSUB tiles.
+// The workgroup of tile 0 also writes the z column and, when asked, u.
+template <int NSUB>
+__global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
+    constexpr int kCols = 512;
+    constexpr int kUIter = 512 / 64;   // q_cat features per lane
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
+    __shared__ __attribute__((aligned(16))) float part[4][kCols];
+    const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
+    const int bg = lin / a.tiles;
+    const int tile = lin - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lo = a.lo, hi = a.lo + a.M;
+    const int cb0 = (lo & ~7) + tile * (kCols * NSUB);
+    const int c_last = (hi - 1) & ~7;   // last 8-column group holding a scanned column (in bounds: C % 8 == 0)
+    const uint16_t* zw = a.zT + ((size_t)bg * 32 + 8 * wave) * a.C;
+
+    // Sub-tile s: this lane's 8 columns of the wave's 8 table rows. Groups past the row end re-read the last group
+    // (in bounds, results discarded), so every sub-tile issues the same eight loads.
+    auto load = [&](int s, u32x4_t (&v)[8]) {
+        const int c0 = min(cb0 + s * kCols + lane * 8, c_last);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            v[jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(zw + (size_t)jj * a.C + c0));
+    };
+    // u[8 wave + c], c < 8: lane -> features lane + 64 i. The weight loads (L2 hits after the first workgroups) are
+    // issued before the table loads: loads retire in issue order, so u can then be built while the table is in flight.
+    // Features past hd re-read feature hd - 1 with q = 0 (no branch, so no wait is placed between the loads).
+    float u[8];
+    u32x4_t vb[2][8];
+    {
+        const uint16_t* qp = a.q_cat + (size_t)bg * a.hd;
+        const uint16_t* wp = a.wq_t + (size_t)g * a.hd * 32 + 8 * wave;
+        uint4 wv[kUIter];
+        float qf[kUIter];
+#pragma unroll
+        for (int it = 0; it < kUIter; ++it) {
+            const int f = lane + 64 * it;
+            const int fc = min(f, a.hd - 1);
+            wv[it] = *reinterpret_cast<const uint4*>(wp + (size_t)fc * 32);
+            qf[it] = bf16_to_f32(qp[fc]);
+            if (f >= a.hd) qf[it] = 0.0f;
+        }
+        load(0, vb[0]);
+        __builtin_amdgcn_sched_barrier(0);   // keep every load above the first use of a weight
+#pragma unroll
+        for (int c = 0; c < 8; ++c) u[c] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < kUIter; ++it) {
+            u[0] += qf[it] * bf16_lo(wv[it].x); u[1] += qf[it] * bf16_hi(wv[it].x);
+            u[2] += qf[it] * bf16_lo(wv[it].y); u[3] += qf[it] * bf16_hi(wv[it].y);
+            u[4] += qf[it] * bf16_lo(wv[it].z); u[5] += qf[it] * bf16_hi(wv[it].z);
+            u[6] += qf[it] * bf16_lo(wv[it].w); u[7] += qf[it] * bf16_hi(wv[it].w);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float x = sum8(u[c]);
+            x += dpp_f32<0x140>(x);   // row_mirror: lane i <-> 15 - i, so the two groups of 8 of each row meet
+            const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+            const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+            const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+            const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+            u[c] = (r0 + r1) + (r2 + r3);
+        }
+    }
+    if (a.hist) clear_histogram<256>(hsh);
+    __syncthreads();
+
+    float* o = a.out + (size_t)bg * a.out_stride - lo;
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+        if (s + 1 < NSUB) load(s + 1, vb[(s + 1) & 1]);
+        const u32x4_t (&v)[8] = vb[s & 1];
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            acc[0] += u[jj] * bf16_lo(v[jj].x);
+            acc[1] += u[jj] * bf16_hi(v[jj].x);
+            acc[2] += u[jj] * bf16_lo(v[jj].y);
+            acc[3] += u[jj] * bf16_hi(v[jj].y);
+            acc[4] += u[jj] * bf16_lo(v[jj].z);
+            acc[5] += u[jj] * bf16_hi(v[jj].z);
+            acc[6] += u[jj] * bf16_lo(v[jj].w);
+            acc[7] += u[jj] * bf16_hi(v[jj].w);
+        }
+        float4* pw = reinterpret_cast<float4*>(&part[wave][lane * 8]);
+        pw[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        pw[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        __syncthreads();
+        const int cc = 2 * tid;
+        const float2 p0 = *reinterpret_cast<const float2*>(&part[0][cc]);
+        const float2 p1 = *reinterpret_cast<const float2*>(&part[1][cc]);
+        const float2 p2 = *reinterpret_cast<const float2*>(&part[2][cc]);
+        const float2 p3 = *reinterpret_cast<const float2*>(&part[3][cc]);
+        const float s0 = (p0.x + p1.x) + (p2.x + p3.x), s1 = (p0.y + p1.y) + (p2.y + p3.y);
+        const int c = cb0 + s * kCols + cc;
+        if (c >= lo && c < hi) {
+            o[c] = s0;
+            if (a.hist) atomicAdd(&hsh[score_key(s0) >> kHistShift], 1u);
+        }
+        if (c + 1 >= lo && c + 1 < hi) {
+            o[c + 1] = s1;
+            if (a.hist) atomicAdd(&hsh[score_key(s1) >> kHistShift], 1u);
+        }
+        if (s + 1 < NSUB) __syncthreads();   // part is rewritten by the next sub-tile
+    }
+    if (tile == 0) {
+        if (a.k_new) write_z<256>(a, bg, g);
+        if (a.u_out && lane < 8) {
+            float uo = u[0];
+#pragma unroll
+            for (int c = 1; c < 8; ++c) uo = lane == c ? u[c] : uo;
+            a.u_out[(size_t)bg * 32 + 8 * wave + lane] = uo;
+        }
+    }
+    if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
+}
+
 // 2-byte-load scan for tables whose rows are not 16-byte aligned: thread -> 8 adjacent columns from lo, never
 // loading at or beyond hi.
 template <int BLOCK>
@@ -615,6 +743,21 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
         launch_prologue(a, BG, s);
         return check_launch("score_prologue");
     }
+    const bool v16_table = vec && (C % 8 == 0) && (reinterpret_cast<uintptr_t>(zT) % 16 == 0);
+    if (u_in == nullptr && v16_table && r == 32 && hd <= 512) {
+        // one launch: u and the z column inside the scan. Sub-tiles per workgroup: as many as keep at least
+        // kFusedMinBlocks workgroups (8 per CU) in the grid.
+        constexpr int kFusedMinBlocks = 2048;
+        const int span = ((hi + 7) & ~7) - (lo & ~7);
+        const int64_t blocks512 = (int64_t)BG * ((span + 511) / 512);
+        const int nsub = blocks512 >= 4 * kFusedMinBlocks ? 4 : blocks512 >= 2 * kFusedMinBlocks ? 2 : 1;
+        a.tiles = (span + 512 * nsub - 1) / (512 * nsub);
+        const dim3 grid(BG * a.tiles), block(256);
+        if (nsub == 4) hipLaunchKernelGGL(score_scan_fused<4>, grid, block, 0, s, a);
+        else if (nsub == 2) hipLaunchKernelGGL(score_scan_fused<2>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(score_scan_fused<1>, grid, block, 0, s, a);
+        return check_launch("score_scan_fused");
+    }
     if (u_in == nullptr && u_out != nullptr) {
         // two launches: u (and the z column) once per (b, g), then a scan that only stages u; the per-block u of the
         // single-launch form costs ~20% of the scan time at B=16, L=32K
@@ -624,7 +767,7 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
         a.u_in = u_out;
         a.k_new = nullptr;
     }
-    const bool v16 = vec && a.u_in != nullptr && (C % 8 == 0) && (reinterpret_cast<uintptr_t>(zT) % 16 == 0);
+    const bool v16 = v16_table && a.u_in != nullptr;
     if (v16) {
         const int span = ((hi + 7) & ~7) - (lo & ~7);
         a.tiles = (span + 511) / 512;

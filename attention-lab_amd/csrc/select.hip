@@ -248,7 +248,7 @@ __device__ __forceinline__ Emitter make_emitter(const SelectArgs& a, int row, Se
 template <int KPT>
 __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
     __shared__ SelectShared sh;
-    const int row = blockIdx.x;
+    const int row = xcd_contiguous_block();   // the XCD whose L2 holds the row's scores after the scan
     const int tid = threadIdx.x;
     const float* s = a.scores + (size_t)row * a.score_stride;
     const int M = a.M;
@@ -352,7 +352,7 @@ __device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared&
 
 __global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a) {
     __shared__ SelectShared sh;
-    select_row_streaming(a, blockIdx.x, sh);
+    select_row_streaming(a, xcd_contiguous_block(), sh);
 }
 
 static int launch_select(const SelectArgs& a, int R, hipStream_t s) {

@@ -67,25 +67,24 @@ def parse_args():
 
 
 PMC_COPY_BYTES = 256 << 20
-PMC_PROFILE = os.path.join(ROOT, "profiles", "score_scan_v16_b16_l32k_pmc.md")
-SCAN_KERNEL = "score_scan_v16"
+PMC_PROFILE = os.path.join(ROOT, "profiles", "score_scan_fused_b16_l32k_pmc.md")
+SCAN_KERNEL = "score_scan_fused"
 
 
 def pmc_workload(torch, dev, args):
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,
                     layers=1, r=args.index_dim, rho=args.rho, seed=args.seed)
     fns = launchers(ls, torch)
-    fns["score"](0)            # u for the scan launches
-    torch.cuda.synchronize()
     for _ in range(5):
-        fns["scan"](0)
+        fns["score"](0)
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_workload": "score_scan_v16 x5 then 256 MiB copy x5", "scan_algorithmic_bytes": ls.scan_bytes(),
-                      "scan_read_bytes": ls.B * ls.G * ls.r * ls.M * 2, "scan_write_bytes": ls.B * ls.G * 4 * ls.M,
+    print(json.dumps({"pmc_workload": f"{SCAN_KERNEL} x5 then 256 MiB copy x5", "scan_algorithmic_bytes": ls.score_bytes(),
+                      "scan_read_bytes": ls.score_bytes() - ls.B * ls.G * (4 * ls.M + 2 * ls.r),
+                      "scan_write_bytes": ls.B * ls.G * (4 * ls.M + 2 * ls.r),
                       "copy_bytes_each_way": PMC_COPY_BYTES}))
     return 0
 
@@ -179,11 +178,9 @@ class LayerStack:
         self.rows = torch.empty(B, G, self.S, device=dev, dtype=torch.int32)
 
     # -- algorithmic bytes per launch (per layer) --
-    def scan_bytes(self):
-        """The scan kernel: index-table columns [lo, hi) read, fp32 scores written (u is 128 B per (b, g))."""
-        return self.B * self.G * (self.r * self.M * 2 + 4 * self.M)
-
     def score_bytes(self):
+        """The score kernel: index-table columns [lo, hi) read and fp32 scores written per (b, g), plus q_cat, k_new and
+        the z column written per (b, g) and the projection weights per group."""
         B, G, h, d, r, M = self.B, self.G, self.h, self.d, self.r, self.M
         return B * G * (r * M * 2 + 4 * M + r * 2 + (h * d + d) * 2) + G * (h * d * r + r * d) * 2
 
@@ -233,15 +230,10 @@ def launchers(ls, torch):
         nat.call("attnlab_dense_decode", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(), B, G,
                  h, ls.L, C, Pd, scale, ls.dense_out[l].data_ptr(), 1, part.data_ptr(), stream())
 
-    def score(l):   # u/z prologue + scan, as in the fused step
+    def score(l):   # u, z column and scan in one launch, as in the fused step: the dominant kernel
         nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
                  ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), None, u_buf.data_ptr(), ls.scores.data_ptr(),
                  ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1, hist.data_ptr(), stream())
-
-    def scan(l):    # the scan kernel alone (u given): the dominant kernel of the step
-        nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), None, None, None, None, u_buf.data_ptr(), None,
-                 ls.scores.data_ptr(), ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1,
-                 hist.data_ptr(), stream())
 
     def select(l):
         nat.call("attnlab_select_rows", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
@@ -257,22 +249,21 @@ def launchers(ls, torch):
                  ls.rows.data_ptr(), ls.S, B, G, h, ls.S, C, P, scale, ls.out[l].data_ptr(), 1, part.data_ptr(),
                  stream())
 
-    return {"sparse": sparse, "dense": dense, "score": score, "scan": scan, "select": select, "attend": attend,
+    return {"sparse": sparse, "dense": dense, "score": score, "select": select, "attend": attend,
             "score_select": score_select, "hist": hist, "partitions": P, "dense_partitions": Pd,
             "_keep": (ws, part, step_hist, u_buf, sel_scratch)}
 
 
 def kernel_breakdown(torch, fns, ls, reps):
-    """Average us per layer of each stage of the fused step, from graphs of 36 launches on consistent data: the
-    scan kernel alone, score (u/z prologue + scan), score + select (the select consumes and clears the histogram the
-    scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend (+ split-K merge)."""
-    t_scan = time_graph(torch, capture(torch, fns["scan"], ls.n), reps, 3) / ls.n
+    """Average us per layer of each stage of the fused step, from graphs of 36 launches on consistent data: score
+    (u, z column and scan, one kernel), score + select (the select consumes and clears the histogram the scan builds;
+    score-only graphs leave it dirty, so it is zeroed before the pair), attend (+ split-K merge)."""
     t_score = time_graph(torch, capture(torch, fns["score"], ls.n), reps, 3) / ls.n
     fns["hist"].zero_()
     torch.cuda.synchronize()
     t_pair = time_graph(torch, capture(torch, fns["score_select"], ls.n), reps, 3) / ls.n
     t_attend = time_graph(torch, capture(torch, fns["attend"], ls.n), reps, 3) / ls.n
-    return {"scan": t_scan * 1e3, "score": t_score * 1e3, "select": (t_pair - t_score) * 1e3,
+    return {"score": t_score * 1e3, "select": (t_pair - t_score) * 1e3,
             "attend": t_attend * 1e3}
 
 
@@ -435,8 +426,7 @@ def main() -> int:
 
     sb, selb, ab, db = ls.score_bytes(), ls.select_bytes(), ls.attend_bytes(), ls.dense_bytes()
     score_us = kus["score"]
-    scan_b = ls.scan_bytes()
-    ach = scan_b / (kus["scan"] * 1e-6) / 1e9
+    ach = sb / (score_us * 1e-6) / 1e9
     us_layer = ms_step * 1e3 / ls.n
     sparse_bytes = sb + selb + ab
     line = {
@@ -460,9 +450,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": f"{SCAN_KERNEL} (candidate scan of the index table)", "achieved": ach,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": ach / PEAK_HBM_GBS,
                      "traffic": measured_traffic() if (ls.B, ls.L, ls.G, ls.r) == (16, 32768, 8, 32) else None,
-                     "algorithmic_bytes_per_launch": scan_b, "avg_launch_us": kus["scan"]},
-        "per_layer_us": {"sparse": us_layer, "dense": ms_dense * 1e3 / ls.n, "score_prologue_and_scan": score_us,
-                         "scan": kus["scan"], "select": kus["select"], "attend_with_combine": kus["attend"]},
+                     "algorithmic_bytes_per_launch": sb, "avg_launch_us": score_us},
+        "per_layer_us": {"sparse": us_layer, "dense": ms_dense * 1e3 / ls.n, "score": score_us,
+                         "select": kus["select"], "attend_with_combine": kus["attend"]},
         "hot_path_hbm": {"algorithmic_bytes_per_layer": sparse_bytes, "gbs": sparse_bytes / (us_layer * 1e-6) / 1e9,
                          "frac_of_peak": sparse_bytes / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBS},
         "kernels": {
