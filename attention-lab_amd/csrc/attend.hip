@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
 // issued before any is used, with an online rescale between groups.
 __global__ __launch_bounds__(1024) void attend_combine(AttendArgs a) {
     constexpr int kGroup = 8;
-    const int bg = blockIdx.x;
+    const int bg = xcd_contiguous_block();   // the XCD whose attend workgroups wrote these partials
     const int h = a.h;
     const float* pb = a.part + (size_t)bg * a.P * h * (kHeadDim + 2);
     for (int idx = threadIdx.x; idx < h * kHeadDim; idx += blockDim.x) {

@@ -42,9 +42,9 @@ struct SelectArgs {
 };
 
 struct SelectShared {
-    uint32_t hist[kHistBins];
+    __attribute__((aligned(16))) uint32_t hist[kHistBins];
     uint32_t wave_tot[kSelWaves][2];
-    uint32_t digit, krem;
+    uint32_t digit, krem, dcount;
     uint64_t sortbuf[kMaxScoreOrderK];
 };
 
@@ -96,6 +96,40 @@ __device__ __forceinline__ void find_digit(SelectShared& sh, const uint32_t* his
     } else if (above + c1 < krem && above + c1 + c0 >= krem) {
         sh.digit = (uint32_t)b0;
         sh.krem = krem - above - c1;
+    }
+    __syncthreads();
+}
+
+// find_digit done by wave 0 alone, for nbins = 1024 or 2048: lane l sums the l-th chunk of nbins / 64 bins from the
+// top (starting at a lane-dependent 16-byte segment, so the lanes spread over the LDS banks), a DPP scan over the
+// lanes finds the chunk holding the krem-th largest key, and a second scan over that chunk's bins, one per lane, finds
+// the bin. Publishes D, the new krem and the count of bin D; one barrier instead of the block scan's three.
+__device__ __forceinline__ void find_digit_wave(SelectShared& sh, const uint32_t* hist, uint32_t krem, int nbins) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int per = nbins >> 6;                 // 16 or 32 bins per lane
+        const int cb = nbins - per * (lane + 1);    // lane 0: the highest chunk
+        const int nseg = per >> 2;
+        uint32_t sum = 0;
+        for (int i = 0; i < nseg; ++i) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hist + cb + 4 * ((lane + i) & (nseg - 1)));
+            sum += (v.x + v.y) + (v.z + v.w);
+        }
+        const uint32_t inc = wave_incl_scan(sum);
+        const uint64_t m = __ballot(inc >= krem);
+        if (m != 0) {
+            const int l0 = __ffsll((unsigned long long)m) - 1;
+            const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), l0);
+            const int top = nbins - per * l0 - 1;    // highest bin of that chunk
+            const uint32_t c = lane < per ? hist[top - lane] : 0u;
+            const uint32_t inc2 = wave_incl_scan(c) + above;
+            const uint64_t m2 = __ballot(lane < per && inc2 >= krem);
+            if (m2 != 0 && lane == __ffsll((unsigned long long)m2) - 1) {
+                sh.digit = (uint32_t)(top - lane);
+                sh.krem = krem - (inc2 - c);
+                sh.dcount = c;
+            }
+        }
     }
     __syncthreads();
 }
@@ -467,7 +501,7 @@ __global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, Ti
 
 __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, TiledArgs t) {
     __shared__ SelectShared sh;                 // sortbuf holds the candidate list (as uint32 indices)
-    __shared__ uint32_t hist3[1024];
+    __shared__ __attribute__((aligned(16))) uint32_t hist3[1024];
     __shared__ uint32_t bits[kMaxWords];
     const int row = xcd_contiguous_block();   // the XCD that classified the row
     const int tid = threadIdx.x;
@@ -486,6 +520,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     if (tid == 0) {   // defaults keep every later index in range even for a state that does not match the scores
         sh.digit = 0u;
         sh.krem = 0u;
+        sh.dcount = 0u;
     }
     uint32_t nc = 0, na = 0;
 #pragma unroll
@@ -532,28 +567,35 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     for (int i = 0; i < kCandPerThread; ++i)
         if (cv[i]) atomicAdd(&sh.hist[low[i] >> 10], 1u);
     __syncthreads();
-    find_digit(sh, sh.hist, krem, 2048);
+    find_digit_wave(sh, sh.hist, krem, 2048);
     const uint32_t d2 = sh.digit & 2047u;
     krem = sh.krem;
 #pragma unroll
     for (int i = 0; i < kCandPerThread; ++i)
         if (cv[i] && (low[i] >> 10) == d2) atomicAdd(&hist3[low[i] & 1023u], 1u);
     __syncthreads();
-    find_digit(sh, hist3, krem, 1024);
+    find_digit_wave(sh, hist3, krem, 1024);
     const uint32_t tlow = (d2 << 10) | (sh.digit & 1023u);
     krem = sh.krem;
-    // equal keys at the threshold: the first krem of them in index order are taken
-    uint32_t neq = 0;
+    if (sh.dcount <= krem) {
+        // every key equal to the threshold is taken (the usual case: no tie at the boundary)
 #pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) neq += cv[i] && low[i] == tlow;
-    uint32_t eeq, unused2, teq, unused_t2;
-    block_scan2<kSelThreads>(neq, 0u, eeq, unused2, teq, unused_t2, sh.wave_tot);
+        for (int i = 0; i < kCandPerThread; ++i)
+            if (cv[i] && low[i] >= tlow) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
+    } else {
+        // equal keys at the threshold: the first krem of them in index order are taken
+        uint32_t neq = 0;
 #pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) {
-        if (!cv[i]) continue;
-        const bool eq = low[i] == tlow;
-        if (low[i] > tlow || (eq && eeq < krem)) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
-        eeq += eq;
+        for (int i = 0; i < kCandPerThread; ++i) neq += cv[i] && low[i] == tlow;
+        uint32_t eeq, unused2, teq, unused_t2;
+        block_scan2<kSelThreads>(neq, 0u, eeq, unused2, teq, unused_t2, sh.wave_tot);
+#pragma unroll
+        for (int i = 0; i < kCandPerThread; ++i) {
+            if (!cv[i]) continue;
+            const bool eq = low[i] == tlow;
+            if (low[i] > tlow || (eq && eeq < krem)) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
+            eeq += eq;
+        }
     }
     __syncthreads();
     // emission: the set bits of this thread's words, in index order
