@@ -167,8 +167,11 @@ def auto_partitions(BG: int, rows: int, *, max_p: int, min_rows: int, blocks: in
     return max(1, min(max_p, want, cap))
 
 
-def sparse_partitions(BG: int, rows: int) -> int:
-    return auto_partitions(BG, rows, max_p=MAX_P, min_rows=128, blocks=256)
+def sparse_partitions(BG: int, rows: int, h: int = 1) -> int:
+    """Split-K count of the sparse read. The kernel also splits each (b, g) over up to h head groups (powers of two
+    dividing h) until the grid reaches one workgroup per CU; those count towards the 256 workgroups."""
+    hg = h & -h if h > 0 else 1   # largest power of two dividing h
+    return auto_partitions(BG * hg, rows, max_p=MAX_P, min_rows=128, blocks=256)
 
 
 def dense_partitions(BG: int, length: int) -> int:
@@ -184,7 +187,7 @@ def attend(q, k, v, rows, *, scale=None, partitions=None, out=None, out_dtype=to
     S = int(rows.shape[2])
     if S < 1:
         raise ValueError("at least one row must be selected")
-    P = sparse_partitions(B * G, S) if partitions is None else int(partitions)
+    P = sparse_partitions(B * G, S, h) if partitions is None else int(partitions)
     if not 1 <= P <= MAX_P:
         raise ValueError(f"partitions must be in [1, {MAX_P}]")
     ws = _SHARED_WS if workspace is None else workspace

@@ -39,6 +39,7 @@ struct AttendArgs {
     int S;  // positions per (b, g): the row list length, or L for the dense read
     int C;  // capacity: listed positions outside [0, C) are skipped, never read
     int h, P;
+    int Q;  // head groups: workgroup (b, g, qg, p) attends heads [qg h/Q, (qg + 1) h/Q) over partition p
     float scale_log2;
     void* out;
     int out_bf16;
@@ -71,20 +72,24 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     __shared__ float red_ml[kMergeSlots][H][2];
     __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
     const int lin = xcd_contiguous_block();   // (b, g) on the XCD that wrote its row list
-    const int bg = lin / a.P;
-    const int p = lin - bg * a.P;
+    const int bg = lin / (a.Q * a.P);
+    const int rem = lin - bg * a.Q * a.P;
+    const int qg = rem / a.P;
+    const int p = rem - qg * a.P;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int slot = lane >> 3;
     const int sub = lane & 7;
-    const int h = a.h;
+    const int h = a.h;          // heads of the KV group (the row stride of q, out and part)
+    const int hq = h / a.Q;     // heads of this workgroup
+    const int h0 = qg * hq;
 
     uint32_t qw[H][8];
 #pragma unroll
     for (int i = 0; i < H; ++i) {
         uint4 x0 = make_uint4(0, 0, 0, 0), x1 = make_uint4(0, 0, 0, 0);
-        if (i < h) {
-            const uint16_t* qp = a.q + ((size_t)bg * h + i) * kHeadDim + 8 * sub;
+        if (i < hq) {
+            const uint16_t* qp = a.q + ((size_t)bg * h + h0 + i) * kHeadDim + 8 * sub;
             x0 = *reinterpret_cast<const uint4*>(qp);
             x1 = *reinterpret_cast<const uint4*>(qp + 64);
         }
@@ -223,7 +228,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         }
     }
     __syncthreads();
-    for (int idx = tid; idx < h * kHeadDim; idx += kAttThreads) {
+    for (int idx = tid; idx < hq * kHeadDim; idx += kAttThreads) {
         const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
         float ms = -INFINITY;
 #pragma unroll
@@ -237,9 +242,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             as += ww * red_acc[w][i][dim];
         }
         if (a.P == 1) {
-            store_out(a, ((size_t)bg * h + i) * kHeadDim + dim, as / ls);
+            store_out(a, ((size_t)bg * h + h0 + i) * kHeadDim + dim, as / ls);
         } else {
-            float* pp = a.part + (((size_t)bg * a.P + p) * h + i) * (kHeadDim + 2);
+            float* pp = a.part + (((size_t)bg * a.P + p) * h + h0 + i) * (kHeadDim + 2);
             if (dim == 0) {
                 pp[0] = ms;
                 pp[1] = ls;
@@ -290,12 +295,23 @@ __global__ __launch_bounds__(1024) void attend_combine(AttendArgs a) {
     }
 }
 
+// Head groups per (b, g): split the h heads over 2, 4, ... workgroups while the grid is below one workgroup per CU.
+// Workgroups of one (b, g) read the same rows at the same time on the same XCD, so the second read of a row comes from
+// L2 (or the Infinity Cache) and HBM traffic stays one read per row; with P = 1 this replaces the split-K merge.
+static int head_groups(int BG, int h, int P) {
+    constexpr int kFillBlocks = 256;
+    int Q = 1;
+    while (h % (2 * Q) == 0 && (int64_t)BG * Q * P < kFillBlocks) Q *= 2;
+    return Q;
+}
+
 template <bool DENSE>
 static int launch_attend(const AttendArgs& a, int BG, hipStream_t s) {
-    const dim3 grid(BG * a.P), block(kAttThreads);
-    if (a.h <= 1) hipLaunchKernelGGL((attend_kernel<1, kStages, DENSE>), grid, block, 0, s, a);
-    else if (a.h <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE>), grid, block, 0, s, a);
-    else if (a.h <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE>), grid, block, 0, s, a);
+    const dim3 grid(BG * a.Q * a.P), block(kAttThreads);
+    const int hq = a.h / a.Q;
+    if (hq <= 1) hipLaunchKernelGGL((attend_kernel<1, kStages, DENSE>), grid, block, 0, s, a);
+    else if (hq <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE>), grid, block, 0, s, a);
+    else if (hq <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attend_kernel<8, kStages, DENSE>), grid, block, 0, s, a);
     if (a.P > 1) hipLaunchKernelGGL(attend_combine, dim3(BG), dim3(a.h * kHeadDim), 0, s, a);
     return check_launch(DENSE ? "dense_decode" : "attend");
@@ -328,7 +344,8 @@ extern "C" int attnlab_attend(const uint16_t* K, const uint16_t* V, int64_t kv_b
     if (rc) return rc;
     ATTNLAB_REQUIRE(S >= 1, "at least one row must be selected (S=%d)", S);
     ATTNLAB_REQUIRE(rows != nullptr && rows_stride >= S, "rows must hold S=%d positions per (b, g)", S);
-    AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, rows, rows_stride, S, C, h, P, scale * kLog2e, out, out_bf16, part};
+    AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, rows, rows_stride, S, C, h, P, head_groups(B * G, h, P),
+                 scale * kLog2e, out, out_bf16, part};
     return launch_attend<false>(a, B * G, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -338,6 +355,7 @@ extern "C" int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_
     const int rc = check_common(K, V, kv_bg_stride, kv_row_stride, q, B, G, h, C, P, out, part);
     if (rc) return rc;
     ATTNLAB_REQUIRE(1 <= L && L <= C, "valid length L=%d outside [1, C=%d]", L, C);
-    AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, nullptr, 0, L, C, h, P, scale * kLog2e, out, out_bf16, part};
+    AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, nullptr, 0, L, C, h, P, head_groups(B * G, h, P),
+                 scale * kLog2e, out, out_bf16, part};
     return launch_attend<true>(a, B * G, reinterpret_cast<hipStream_t>(stream));
 }

@@ -203,7 +203,7 @@ def launchers(ls, torch):
     lib = nat.lib()
     dev = ls.K[0].device
     B, G, h, d, r, C = ls.B, ls.G, ls.h, ls.d, ls.r, ls.C
-    P = hip_attend.sparse_partitions(B * G, ls.S)
+    P = hip_attend.sparse_partitions(B * G, ls.S, h)
     Pd = hip_attend.dense_partitions(B * G, ls.L)
     ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
