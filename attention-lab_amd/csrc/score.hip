@@ -314,10 +314,11 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
 // The v16 scan with the prologue folded in (r = 32, q_cat features hd <= 512, 16-byte aligned operands): one launch per
 // step instead of two, which saves a kernel boundary (a few microseconds of launch, drain and cache maintenance on
 // MI355X, more than the prologue's own work). Wave w needs u[j] only for its own j in [8w, 8w + 8): it reads those 8
-// weights of every q_cat feature (one 16-byte load per feature, 8 KB per wave, L2-resident) right after its first
-// table loads are in flight, and reduces them in registers (DPP within rows of 16 lanes, then readlane), so u costs no
-// barrier. A workgroup covers NSUB consecutive 512-column sub-tiles, double-buffered (the loads of sub-tile s + 1 are
-// issued before sub-tile s is reduced), which spreads the weight reads and the histogram flush over NSUB tiles.
+// weights of every q_cat feature (one 16-byte load per feature, 8 KB per wave, L2-resident) just before its first
+// table loads, and reduces them in registers (DPP within rows of 16 lanes, then readlane) while the table is in
+// flight, so u costs no barrier. A workgroup covers NSUB 512-column sub-tiles of its row, `tiles` sub-tiles apart,
+// double-buffered (the loads of sub-tile s + 1 are issued before sub-tile s is reduced), which spreads the weight reads
+// and the histogram flush over NSUB sub-tiles.
 // The workgroup of tile 0 also writes the z column and, when asked, u.
 template <int NSUB>
 __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
@@ -332,14 +333,17 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lo = a.lo, hi = a.lo + a.M;
-    const int cb0 = (lo & ~7) + tile * (kCols * NSUB);
+    // sub-tile s of workgroup `tile` is the row's 512-column sub-tile s * tiles + tile: at each step the workgroups of a
+    // row read one contiguous stretch of every table row, as a grid of one-tile workgroups would
+    const int cb0 = (lo & ~7) + tile * kCols;
+    const int sstride = a.tiles * kCols;
     const int c_last = (hi - 1) & ~7;   // last 8-column group holding a scanned column (in bounds: C % 8 == 0)
     const uint16_t* zw = a.zT + ((size_t)bg * 32 + 8 * wave) * a.C;
 
     // Sub-tile s: this lane's 8 columns of the wave's 8 table rows. Groups past the row end re-read the last group
     // (in bounds, results discarded), so every sub-tile issues the same eight loads.
     auto load = [&](int s, u32x4_t (&v)[8]) {
-        const int c0 = min(cb0 + s * kCols + lane * 8, c_last);
+        const int c0 = min(cb0 + s * sstride + lane * 8, c_last);
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
             v[jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(zw + (size_t)jj * a.C + c0));
@@ -416,7 +420,7 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         const float2 p2 = *reinterpret_cast<const float2*>(&part[2][cc]);
         const float2 p3 = *reinterpret_cast<const float2*>(&part[3][cc]);
         const float s0 = (p0.x + p1.x) + (p2.x + p3.x), s1 = (p0.y + p1.y) + (p2.y + p3.y);
-        const int c = cb0 + s * kCols + cc;
+        const int c = cb0 + s * sstride + cc;
         if (c >= lo && c < hi) {
             o[c] = s0;
             if (a.hist) atomicAdd(&hsh[score_key(s0) >> kHistShift], 1u);
