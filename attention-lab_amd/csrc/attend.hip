@@ -67,7 +67,7 @@ struct KVStage {
 
 template <int H, int D, bool DENSE>
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
-    constexpr int kChunk = 1024;   // row-list entries whose positions are staged in LDS at a time
+    constexpr int kChunk = 4096;   // row-list entries whose positions are staged in LDS at a time (one chunk for k <= 4096)
     __shared__ int idx_sh[DENSE ? 1 : kChunk];
     __shared__ float red_ml[kMergeSlots][H][2];
     __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
