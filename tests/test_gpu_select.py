@@ -157,6 +157,29 @@ def state_for(s):
     return torch.from_numpy(st.astype(np.int32))
 
 
+@pytest.mark.parametrize("B,C,lo,hi,fused", [(2, 32768, 4, 32704, True), (2, 32768, 4, 32704, False),
+                                             (1, 3000, 4, 2900, True), (3, 1000, 0, 1000, False)])
+def test_score_kernel_hands_over_the_first_digit_histogram(gpu, B, C, lo, hi, fused):
+    """The state the score kernel leaves is exactly the histogram of its own scores' first 11-bit digits (counted
+    once per score, whatever the workgroup split) followed by its 64 super-bin sums."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_score
+    from attention_lab.indexer import GroupedIndexer
+    G, r, h, d = 8, 32, 4, 128
+    gen = torch.Generator().manual_seed(B * 7 + C)
+    zT = torch.randn(B, G, r, C, generator=gen).to(torch.bfloat16).to(gpu)
+    state = torch.zeros(B, G, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    if fused:
+        idx = GroupedIndexer(G, h, d, r, device=gpu, dtype=torch.bfloat16, seed=3)
+        q_cat = torch.randn(B, G, h * d, generator=gen).to(torch.bfloat16).to(gpu)
+        s = hip_score.score_grouped(zT, lo, hi, q_cat=q_cat, wq_t=idx.wq_t_scaled, state=state)
+    else:
+        u = torch.randn(B, G, r, generator=gen).to(gpu)
+        s = hip_score.score_grouped(zT, lo, hi, u=u, state=state)
+    torch.cuda.synchronize()
+    assert torch.equal(state.cpu(), state_for(s.cpu().numpy()))
+
+
 def tie_heavy(rng, shape):
     return rng.integers(0, 6, size=shape).astype(np.float32) * 0.25
 
