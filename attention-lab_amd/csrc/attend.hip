@@ -68,7 +68,7 @@ struct KVStage {
 template <int H, int D, bool DENSE>
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     constexpr int kChunk = 4096;   // row-list entries whose positions are staged in LDS at a time (one chunk for k <= 4096)
-    __shared__ int idx_sh[DENSE ? 1 : kChunk];
+    __shared__ __attribute__((aligned(16))) int idx_sh[DENSE ? 4 : kChunk];
     __shared__ float red_ml[kMergeSlots][H][2];
     __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
     const int lin = xcd_contiguous_block();   // (b, g) on the XCD that wrote its row list
@@ -117,8 +117,16 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     for (int c0 = s_begin; c0 < s_end; c0 += chunk) {
         const int clen = min(chunk, s_end - c0);
         if (!DENSE) {
-            __syncthreads();   // every wave is done with the previous chunk's positions
-            for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = rl[c0 + i];
+            if (c0 != s_begin) __syncthreads();   // every wave is done with the previous chunk's positions
+            const int32_t* src = rl + c0;
+            if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {   // 16-byte loads where the chunk is aligned
+                const int nv = clen >> 2;
+                for (int i = tid; i < nv; i += kAttThreads)
+                    reinterpret_cast<int4*>(idx_sh)[i] = reinterpret_cast<const int4*>(src)[i];
+                for (int i = 4 * nv + tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+            } else {
+                for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+            }
             __syncthreads();
         }
         // The chunk's entries form groups of 8 (one per slot of a wave); wave w takes groups w, w + kAttWaves, ...
