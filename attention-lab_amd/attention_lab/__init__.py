@@ -4,6 +4,7 @@ The import surface mirrors the reference package (src/attention_lab/__init__.py:
 switches by putting `attention-lab_amd/` on sys.path instead of `src/`. The Metal modules' counterparts are
 `hip_score` (MetalScore) and `hip_attend` (MetalAttend); `hip_select` is the top-k kernel the reference never built.
 Importing needs only torch; the kernels load from libattnlab.so on first use and every op raises when it is absent.
+The Qwen3 wrapper (`qwen_wrap`) needs transformers and is imported explicitly, as in the reference.
 """
 __version__ = "0.1.0"
 IMPLEMENTATION_STATUS = "mi355x_sparse_decode_hot_path"
@@ -14,7 +15,8 @@ from .sparse import flatten_cache, gather_attention, gather_rows, row_offsets  #
 from .full import FULL_BACKENDS, full_attention  # noqa: E402
 from .indexer import GroupedIndexer, candidate_scores, project_keys, project_queries  # noqa: E402
 from .decode import (DecodeRequest, dense_decode_step, gathered_decode_step_kernel, prepare_request,  # noqa: E402
-                     select_rows_kernel, sparse_decode_step, sparse_decode_step_kernel)
+                     select_rows_kernel, select_rows_recent, select_rows_uniform, sparse_decode_step,
+                     sparse_decode_step_kernel)
 
 __all__ = [
     "FIXED_PREFIX", "FIXED_RECENT", "SelectionLayout", "fixed_budget", "legal_length", "selection_layout",
@@ -22,5 +24,5 @@ __all__ = [
     "FULL_BACKENDS", "full_attention",
     "GroupedIndexer", "candidate_scores", "project_keys", "project_queries",
     "DecodeRequest", "dense_decode_step", "gathered_decode_step_kernel", "prepare_request", "select_rows_kernel",
-    "sparse_decode_step", "sparse_decode_step_kernel",
+    "select_rows_recent", "select_rows_uniform", "sparse_decode_step", "sparse_decode_step_kernel",
 ]

@@ -121,6 +121,39 @@ def select_rows_kernel(u, zT, fixed_rows, off_lo, lo: int, hi: int, k: int) -> t
     return flat
 
 
+def select_rows_recent(fixed_rows, off_lo, lo: int, hi: int, k: int) -> torch.Tensor:
+    """B selector (reference decode.py:96-109): the k most recent candidates [hi - k, hi) after F, as flat row ids.
+
+    Candidate-relative index i maps to row off_lo + i, as the top-k indices of the index selector do; nothing is scored.
+    """
+    B, G = fixed_rows.shape[:2]
+    if k <= 0:
+        return fixed_rows.reshape(-1)
+    M = hi - lo
+    if k > M:
+        raise ValueError(f"k={k} exceeds the candidate count {M}")
+    rel = torch.arange(M - k, M, device=fixed_rows.device, dtype=torch.long).expand(B, G, k)
+    return torch.cat([fixed_rows, rel + off_lo], dim=-1).reshape(-1)
+
+
+def select_rows_uniform(fixed_rows, off_lo, lo: int, hi: int, k: int, *, rng) -> torch.Tensor:
+    """C selector (reference decode.py:112-128): k candidates drawn uniformly without replacement per (b, g), after F.
+
+    `rng` is a numpy Generator; the draw is the top k of B*G*M float64 uniforms taken from it in one call, so a given
+    generator state yields the reference's rows. Not a learned choice.
+    """
+    import numpy as np   # the package stays importable without numpy
+    B, G = fixed_rows.shape[:2]
+    if k <= 0:
+        return fixed_rows.reshape(-1)
+    M = hi - lo
+    if k > M:
+        raise ValueError(f"k={k} exceeds the candidate count {M}")
+    draws = torch.from_numpy(rng.random((B, G, M), dtype=np.float64))
+    rel = torch.topk(draws, k, dim=-1).indices.to(fixed_rows.device)
+    return torch.cat([fixed_rows, rel + off_lo], dim=-1).reshape(-1)
+
+
 def _positions_from_flat(rows, B, G, S, C, device):
     off = row_offsets(B, G, C, device)
     pos = rows.view(B, G, S) - off

@@ -1,11 +1,16 @@
-"""Full attention A over every legal position, for one decode query, on the dense decode kernel.
+"""Full attention A over every legal position, on the dense decode kernel.
 
 Same signature and validation as the reference's full_attention (src/attention_lab/full.py:14-44). Every backend
 name of the reference is accepted; all of them read K and V once per KV group (the reference's sdpa_fold
 behaviour), which is the only layout the HIP kernel has. A single query at the last legal position needs no mask
-(full.py:29). Multi-query (prefill) attention is not part of the HIP decode path and raises NotImplementedError.
+(full.py:29). Several queries (a prefill chunk) follow the reference's legality rule (reference.py:41-48: key j is
+legal for query t iff j <= its position and j < valid_length): query t is one dense-decode launch over the first
+min(position_t + 1, valid_length) positions. That is exact and stays on the HIP kernel, at one launch per query
+position; a prefill GEMM kernel is not part of this build.
 """
 from __future__ import annotations
+
+import torch
 
 from . import hip_attend
 
@@ -24,7 +29,7 @@ def _check_shapes(q, k, v):
 
 
 def full_attention(q, k, v, *, valid_length=None, query_positions=None, scale=None, backend="sdpa_fold"):
-    """q [B,G,h,1,d]; k, v [B,G,C,d]; reads k[:, :, :valid_length]. Returns [B,G,h,1,d]."""
+    """q [B,G,h,T,d]; k, v [B,G,C,d]; reads k[:, :, :valid_length]. Returns [B,G,h,T,d]."""
     B, G, h, T, d, C = _check_shapes(q, k, v)
     legal = C if valid_length is None else int(valid_length)
     if not 0 < legal <= C:
@@ -37,8 +42,11 @@ def full_attention(q, k, v, *, valid_length=None, query_positions=None, scale=No
         raise ValueError(f"need {T} query positions, got {len(qp)}")
     if min(qp) < 0:
         raise ValueError("query positions must be non-negative")
-    if T != 1 or qp[0] < legal - 1:
-        raise NotImplementedError("the HIP path reads one decode query at the last legal position; "
-                                  "multi-query (prefill) attention is not part of it")
-    out = hip_attend.dense_decode(q.reshape(B, G, h, d).contiguous(), k, v, legal, scale=scale, out_dtype=q.dtype)
-    return out.view(B, G, h, 1, d)
+    if T == 1 and qp[0] >= legal - 1:
+        out = hip_attend.dense_decode(q.reshape(B, G, h, d).contiguous(), k, v, legal, scale=scale, out_dtype=q.dtype)
+        return out.view(B, G, h, 1, d)
+    out = torch.empty(B, G, h, T, d, dtype=q.dtype, device=q.device)
+    for t, p in enumerate(qp):
+        out[:, :, :, t] = hip_attend.dense_decode(q[:, :, :, t].contiguous(), k, v, min(p + 1, legal), scale=scale,
+                                                  out_dtype=q.dtype)
+    return out

@@ -141,6 +141,19 @@ def dense_attention(q, K, V, valid_length: int, scale=None) -> np.ndarray:
     return np.einsum("bgic,bgcd->bgid", _softmax_rows(s), V[:, :, :valid_length])
 
 
+def causal_attention(q, K, V, valid_length: int, query_positions=None, scale=None) -> np.ndarray:
+    """Full read A for T queries (a prefill chunk), reference.py:28-62: key j is legal for query t iff
+    j <= query_positions[t] and j < valid_length; by default the queries are the last T legal positions.
+    q [B,G,h,T,d] -> [B,G,h,T,d]. Written with an additive -inf mask over [0, valid_length)."""
+    B, G, h, T, d = q.shape
+    qp = np.arange(valid_length - T, valid_length) if query_positions is None else np.asarray(query_positions)
+    sc = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    s = np.einsum("bgitd,bgcd->bgitc", q, K[:, :, :valid_length]) * sc
+    legal = np.arange(valid_length)[None, :] <= qp[:, None]            # [T, L]
+    s = np.where(legal[None, None, None], s, -np.inf)
+    return np.einsum("bgitc,bgcd->bgitd", _softmax_rows(s), V[:, :, :valid_length])
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # whole D step (decode.py:145-163)
 # ---------------------------------------------------------------------------------------------------------------------

@@ -222,10 +222,21 @@ def test_full_attention_contract(gpu):
         full_attention(q5, K4, V4, valid_length=200)
     with pytest.raises(ValueError):
         full_attention(q5, K4, V4, backend="flash")
-    with pytest.raises(NotImplementedError):
-        full_attention(torch.cat([q5, q5], dim=3), K4, V4, valid_length=64)
-    with pytest.raises(NotImplementedError):
-        full_attention(q5, K4, V4, valid_length=64, query_positions=[10])
+    with pytest.raises(ValueError):
+        full_attention(torch.cat([q5, q5], dim=3), K4, V4, valid_length=64, query_positions=[10])
+    with pytest.raises(ValueError):
+        full_attention(q5, K4, V4, valid_length=64, query_positions=[-1])
+    # several queries (a prefill chunk): the reference's legality rule, key j legal iff j <= position and j < L
+    q4 = torch.cat([q5, q5.flip(2), q5 * 0.5, -q5], dim=3)
+    for L, qp in ((64, None), (50, [0, 17, 49, 60]), (64, [63, 2, 31, 31])):
+        out = full_attention(q4, K4, V4, valid_length=L, query_positions=qp)
+        torch.cuda.synchronize()
+        want = exact.causal_attention(f64(q4), f64(K4), f64(V4), L, qp)
+        assert float(np.abs(f64(out) - want).max()) <= 2e-2, f"L={L} positions={qp}"
+    # one query before the last legal position reads only up to itself
+    out = full_attention(q5, K4, V4, valid_length=64, query_positions=[10])
+    torch.cuda.synchronize()
+    assert float(np.abs(f64(out) - exact.causal_attention(f64(q5), f64(K4), f64(V4), 64, [10])).max()) <= 2e-2
     # a single query over the whole history: no square causal mask (test_attention_contracts.py:211-228)
     L = 37
     out = full_attention(q5, K4, V4, valid_length=L)

@@ -260,3 +260,22 @@ def test_planted_mistakes_are_caught():
     # 4. a softmax that drops the scale differs from the reference scale
     sub = exact.subset_attention(q, K, V, rows)
     assert np.abs(sub - exact.subset_attention(q, K, V, rows, scale=1.0)).max() > 1e-4
+
+
+def test_causal_attention_is_one_dense_read_per_query():
+    """The masked formulation of the prefill read equals, query by query, the sliced dense read over the first
+    min(position + 1, valid_length) keys; a single last-position query is exactly dense_attention."""
+    rng = np.random.default_rng(11)
+    B, G, h, T, d, C = 2, 3, 2, 5, 16, 40
+    q = rng.standard_normal((B, G, h, T, d))
+    K, V = rng.standard_normal((B, G, C, d)), rng.standard_normal((B, G, C, d))
+    for L, qp in ((30, None), (30, [0, 7, 29, 29, 35]), (40, [3, 3, 12, 39, 1])):
+        got = exact.causal_attention(q, K, V, L, qp)
+        pos = list(range(L - T, L)) if qp is None else qp
+        for t, p in enumerate(pos):
+            want = exact.dense_attention(q[:, :, :, t], K, V, min(p + 1, L))
+            np.testing.assert_allclose(got[:, :, :, t], want, atol=1e-12)
+    np.testing.assert_allclose(exact.causal_attention(q[:, :, :, :1], K, V, 30)[:, :, :, 0],
+                               exact.dense_attention(q[:, :, :, 0], K, V, 30), atol=1e-12)
+    first = exact.causal_attention(q, K, V, 30, [0, 0, 0, 0, 0])          # position 0 reads only key 0
+    np.testing.assert_allclose(first, np.broadcast_to(V[:, :, None, None, 0], first.shape), atol=1e-12)
