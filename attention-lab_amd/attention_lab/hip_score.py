@@ -248,6 +248,51 @@ def score_lightning(keys, q, w, lo: int = 0, hi=None, *, relu: bool = True, out=
     return out[..., :M]
 
 
+def score_lightning_batched(keys, q, w, lo: int = 0, hi=None, *, q_pos0=None, relu: bool = True, out=None):
+    """Batched (prefill) lightning score on the matrix cores, T queries per (b, kg):
+    out[b,kg,t,m-lo] = sum_i w[b,kg,t,i] * act(q[b,kg,t,i] . keys[b,kg,m]) for m in [lo, hi).
+
+    keys [B,KG,L,32] fp16 or bf16 contiguous; q [B,KG,T,nh,32] fp32 contiguous; w [B,KG,T,nh] fp32; nh in {1,2,4,8}.
+    q_pos0: when given, query t sits at position q_pos0 + t and reads only keys m <= q_pos0 + t; the scores past that
+    bound are not written (they keep whatever `out` held). out: optional fp32 [B,KG,T,>=hi-lo] contiguous tensor whose
+    last dimension is a multiple of 4. Returns the fp32 [B, KG, T, hi-lo] view.
+    """
+    if keys.dim() != 4 or keys.shape[3] != 32 or keys.dtype not in (torch.float16, torch.bfloat16) \
+            or not keys.is_contiguous() or not keys.is_cuda:
+        raise ValueError("keys must be a contiguous fp16/bf16 [B, KG, L, 32] tensor on a HIP device")
+    B, KG, L, r = keys.shape
+    if q.dim() != 5 or tuple(q.shape[:2]) != (B, KG) or q.shape[4] != r or q.dtype != torch.float32 \
+            or not q.is_contiguous():
+        raise ValueError("q must be a contiguous float32 [B, KG, T, nh, 32] tensor")
+    T, nh = int(q.shape[2]), int(q.shape[3])
+    if nh not in (1, 2, 4, 8):
+        raise ValueError(f"index heads nh={nh} must be 1, 2, 4 or 8")
+    if tuple(w.shape) != (B, KG, T, nh) or w.dtype != torch.float32 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous float32 [B, KG, T, nh] tensor")
+    for t, n in ((q, "q"), (w, "w")):
+        _on_device(t, keys, n)
+    hi = L if hi is None else int(hi)
+    lo = int(lo)
+    if not 0 <= lo <= hi <= L:
+        raise ValueError(f"need 0 <= lo <= hi <= L, got lo={lo} hi={hi} L={L}")
+    if q_pos0 is not None and int(q_pos0) < 0:
+        raise ValueError(f"q_pos0={q_pos0} must be >= 0")
+    M = hi - lo
+    if out is None:
+        out = torch.empty(B, KG, T, max((M + 3) // 4 * 4, 4), dtype=torch.float32, device=keys.device)
+    elif out.dtype != torch.float32 or out.dim() != 4 or tuple(out.shape[:3]) != (B, KG, T) or out.shape[3] < M \
+            or out.shape[3] % 4 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float32 [{B}, {KG}, {T}, >= {M}] tensor with a last dimension "
+                         "that is a multiple of 4")
+    else:
+        _on_device(out, keys, "out")
+    dt = nat.DT_F16 if keys.dtype == torch.float16 else nat.DT_BF16
+    nat.call("attnlab_score_lightning_batched", keys.data_ptr(), dt, q.data_ptr(), w.data_ptr(), out.data_ptr(),
+             out.shape[3], B, KG, L, r, nh, T, lo, hi, -1 if q_pos0 is None else int(q_pos0), int(bool(relu)),
+             nat.stream_of(keys.device))
+    return out[..., :M]
+
+
 def scale_for(r: int) -> float:
     """The 1/sqrt(r) the reference folds into wq_t_scaled (indexer.py:45)."""
     return 1.0 / math.sqrt(r)

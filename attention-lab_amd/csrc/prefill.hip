@@ -1,0 +1,267 @@
+// Batched (prefill) lightning-indexer scores on the matrix cores of gfx950: T queries of one (b, kg) against its keys,
+//   out[b,kg,t,m-lo] = sum_i w[b,kg,t,i] * act(q[b,kg,t,i,:] . key[b,kg,m,:])   m in [lo, hi), m <= q_pos0 + t if causal
+// It is the T-query form of attnlab_score_lightning (one query per (b, kg), HBM-bound, no MFMA). With T queries the
+// contraction over r = 32 is a real GEMM, [T*nh, 32] x [32, M], so it runs on v_mfma_f32_16x16x32_{f16,bf16}; the
+// head reduction, ReLU and weights are applied to the accumulators in registers and only the fp32 scores leave the
+// CU. The fp32 queries are split into a 16-bit head and a 16-bit remainder (q = hi + lo) and both are multiplied, so
+// the result keeps fp32 accuracy (the remainder's rounding error is about 2^-22 of |q|).
+//
+// The kernel writes T*M*4 bytes and reads the keys once per 64-query tile (from L2 after the first), so at any T above
+// a few dozen it is bound by the score writes to HBM, not by the matrix cores: one 16x16x32 MFMA pair makes 16 x 16
+// dot products = 1 KB of scores at nh = 4 for 32 Kflop, which at 8 TB/s of writes asks for a quarter of the MFMA peak.
+#include <type_traits>
+
+#include "common.h"
+
+namespace attnlab {
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+
+struct LightningBatchArgs {
+    const uint16_t* keys;   // [BKG, Lk, 32] fp16 or bf16
+    const float* q;         // [BKG, T, nh, 32]
+    const float* w;         // [BKG, T, nh]
+    float* out;             // row (bkg, t) at out + (bkg * T + t) * out_stride; column m - lo
+    int64_t out_stride;     // multiple of 4
+    int Lk, T, lo, hi;
+    int q_pos0;             // causal: query t reads keys m <= q_pos0 + t; negative: no causal bound
+    int relu;
+    int qtiles, ktiles;
+};
+
+constexpr int kQTile = 64;     // queries per workgroup: 16 per wave
+constexpr int kKBlock = 64;    // keys per step of a wave: four 16-column MFMA tiles
+constexpr int kKTile = 1024;   // keys per workgroup
+
+// 8 consecutive fp32 -> (head, remainder) 16-bit vectors, both rounded to nearest even.
+template <bool F16>
+__device__ __forceinline__ void split8(const float4& x0, const float4& x1,
+                                       std::conditional_t<F16, f16x8_t, bf16x8_t>& hi,
+                                       std::conditional_t<F16, f16x8_t, bf16x8_t>& lo) {
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if constexpr (F16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            hi[e] = (_Float16)x[e];
+            lo[e] = (_Float16)(x[e] - (float)hi[e]);
+        }
+    } else {
+        u16x8_t h, l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h[e] = f32_to_bf16_rne(x[e]);
+            l[e] = f32_to_bf16_rne(x[e] - bf16_to_f32(h[e]));
+        }
+        hi = __builtin_bit_cast(bf16x8_t, h);
+        lo = __builtin_bit_cast(bf16x8_t, l);
+    }
+}
+
+// max(x, 0) as one integer max: negative numbers and -0.0 have the sign bit set, so they compare below 0.
+__device__ __forceinline__ float relu(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma16x16x32(const std::conditional_t<F16, f16x8_t, bf16x8_t>& a,
+                                                const std::conditional_t<F16, f16x8_t, bf16x8_t>& b, f32x4_t c) {
+    if constexpr (F16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Workgroup = 64 queries x 1024 keys of one (b, kg); wave w owns queries [16 w, 16 w + 16) of the tile and walks the
+// keys 64 at a time. MFMA operands (lane l, n = l & 15, K elements 8 (l >> 4) .. + 7):
+//   A row n    = (query n / nh, head n % nh) of one row group of 16 / nh queries; the wave has nh such groups
+//   B column n = key m0 + 4 n + c for the c-th of four tiles, so after the four tiles a lane holds 4 adjacent keys
+//   D          lane l holds rows 4 (l >> 4) + i, i < 4, of column n
+// so every lane ends with whole heads of 4 / nh queries (nh = 8: half the heads, the other half in lane l ^ 16) and
+// writes them as one 16-byte store of 4 adjacent scores per query. The keys of the next step are loaded before the
+// current step's MFMAs.
+template <bool F16, int NH, bool RELU>
+__global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
+    using vec8 = std::conditional_t<F16, f16x8_t, bf16x8_t>;
+    constexpr int QG = 16 / NH;             // queries per row group
+    constexpr int NG = NH;                  // row groups per wave (16 queries)
+    constexpr int QPL = NH >= 4 ? 1 : 4 / NH;   // queries per lane per row group
+    constexpr int HPL = NH >= 4 ? 4 : NH;       // heads per lane per query
+    const int lin = xcd_contiguous_block();   // a (b, kg)'s tiles on one XCD: its keys stay in that L2
+    const int kt = lin % a.ktiles;
+    const int rest = lin / a.ktiles;
+    const int qt = rest % a.qtiles;
+    const int bkg = rest / a.qtiles;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t_wave = qt * kQTile + wave * 16;
+    const int m_begin = a.lo + kt * kKTile;
+    int m_end = min(a.hi, m_begin + kKTile);
+    if (a.q_pos0 >= 0) m_end = min(m_end, a.q_pos0 + min(t_wave + 15, a.T - 1) + 1);
+    if (t_wave >= a.T || m_begin >= m_end) return;   // whole wave: nothing of it is visible (no barrier below)
+
+    const int n = lane & 15, kq = lane >> 4;
+    vec8 ahi[NG], alo[NG];
+    float wv[NG][4];
+    const float* qb = a.q + (size_t)bkg * a.T * NH * 32;
+    const float* wb = a.w + (size_t)bkg * a.T * NH;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int t = min(t_wave + g * QG + n / NH, a.T - 1);   // rows past T compute on the last query, not stored
+        const float4* src = reinterpret_cast<const float4*>(qb + ((size_t)t * NH + n % NH) * 32 + 8 * kq);
+        split8<F16>(src[0], src[1], ahi[g], alo[g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = 4 * kq + i;
+            const int tt = min(t_wave + g * QG + rr / NH, a.T - 1);
+            wv[g][i] = wb[(size_t)tt * NH + rr % NH];
+        }
+    }
+
+    const uint16_t* kbase = a.keys + (size_t)bkg * a.Lk * 32 + 8 * kq;
+    auto load_keys = [&](int m0, vec8 (&b)[4]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int m = min(m0 + 4 * n + c, a.Lk - 1);   // past the range: a real key, result not stored
+            b[c] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4_t*>(kbase + (size_t)m * 32));
+        }
+    };
+    float* ob = a.out + (size_t)bkg * a.T * a.out_stride - a.lo;
+    const bool causal = a.q_pos0 >= 0;
+    // Scores of row group g against the four key tiles in b: v[p][c] = score of the lane's p-th query and key
+    // m0 + 4 n + c (nh = 8: the sum over both lane halves' heads, in both lanes).
+    auto scores = [&](int g, const vec8 (&b)[4], f32x4_t (&v)[QPL]) {
+        f32x4_t acc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            acc[c] = mfma16x16x32<F16>(ahi[g], b[c], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+            acc[c] = mfma16x16x32<F16>(alo[g], b[c], acc[c]);
+        }
+#pragma unroll
+        for (int p = 0; p < QPL; ++p) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float x = 0.0f;
+#pragma unroll
+                for (int i = p * HPL; i < p * HPL + HPL; ++i) x += wv[g][i] * (RELU ? relu(acc[c][i]) : acc[c][i]);
+                if constexpr (NH == 8) x += shfl_xor_f32(x, 16);
+                v[p][c] = x;
+            }
+        }
+    };
+    // nh = 8: the two lanes holding a query's halves store two scores each, so every lane stores
+    const int half = NH == 8 ? 2 * (kq & 1) : 0;
+
+    // Interior blocks (every key visible to every query of the wave): unconditional stores, so the wait for the next
+    // block's keys counts exactly the stores issued after them. Then at most a couple of boundary blocks (the causal
+    // diagonal, the row end, queries past T) with per-score masks.
+    int m_int = m_begin;
+    if (t_wave + 15 < a.T) {
+        int lim = min(a.hi, m_begin + kKTile);
+        if (causal) lim = min(lim, a.q_pos0 + t_wave + 1);
+        m_int = m_begin + max(0, (lim - m_begin) / kKBlock) * kKBlock;
+    }
+    // row pointers of the lane's queries for the interior blocks, which exist only when all 16 queries are below T
+    float* rowp[NG][QPL];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int p = 0; p < QPL; ++p)
+            rowp[g][p] = ob + (size_t)min(t_wave + g * QG + (4 * kq) / NH + p, a.T - 1) * a.out_stride + 4 * n + half;
+    auto store_block = [&](int m0, const vec8 (&b)[4]) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            f32x4_t v[QPL];
+            scores(g, b, v);
+#pragma unroll
+            for (int p = 0; p < QPL; ++p) {
+                float* dst = rowp[g][p] + m0;
+                if constexpr (NH == 8) {
+                    const f32x2_t h2 = half ? f32x2_t{v[p][2], v[p][3]} : f32x2_t{v[p][0], v[p][1]};
+                    __builtin_nontemporal_store(h2, reinterpret_cast<f32x2_t*>(dst));
+                } else {
+                    __builtin_nontemporal_store(v[p], reinterpret_cast<f32x4_t*>(dst));
+                }
+            }
+        }
+    };
+    vec8 ka[4], kb[4];
+    load_keys(m_begin, ka);
+    int m0 = m_begin;
+    for (; m0 + kKBlock < m_int; m0 += 2 * kKBlock) {   // two blocks per trip: the buffers swap roles, no copies
+        load_keys(m0 + kKBlock, kb);
+        store_block(m0, ka);
+        load_keys(m0 + 2 * kKBlock, ka);
+        store_block(m0 + kKBlock, kb);
+    }
+    if (m0 < m_int) {   // an odd interior block
+        load_keys(m0 + kKBlock, kb);
+        store_block(m0, ka);
+        m0 += kKBlock;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ka[c] = kb[c];
+    }
+    vec8 (&cur)[4] = ka;
+    for (; m0 < m_end; m0 += kKBlock) {
+        const int mk = m0 + 4 * n;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            f32x4_t v[QPL];
+            scores(g, cur, v);
+#pragma unroll
+            for (int p = 0; p < QPL; ++p) {
+                const int t = t_wave + g * QG + (4 * kq) / NH + p;
+                if (t >= a.T) continue;
+                const int limit = causal ? min(a.hi, a.q_pos0 + t + 1) : a.hi;
+                float* dst = ob + (size_t)t * a.out_stride + mk;
+#pragma unroll
+                for (int c = half; c < (NH == 8 ? half + 2 : 4); ++c)
+                    if (mk + c < limit) dst[c] = v[p][c];
+            }
+        }
+        load_keys(m0 + kKBlock, cur);
+    }
+}
+
+}  // namespace
+}  // namespace attnlab
+
+using namespace attnlab;
+
+extern "C" int attnlab_score_lightning_batched(const uint16_t* keys, int key_dtype, const float* q, const float* w,
+                                               float* out, int64_t out_stride, int B, int KG, int Lk, int r, int nh,
+                                               int T, int lo, int hi, int q_pos0, int relu, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && KG >= 1 && T >= 0, "B, KG must be positive and T >= 0 (B=%d KG=%d T=%d)", B, KG, T);
+    ATTNLAB_REQUIRE(r == 32, "lightning keys must have r == 32, got %d", r);
+    ATTNLAB_REQUIRE(nh == 1 || nh == 2 || nh == 4 || nh == 8, "index heads nh=%d must be 1, 2, 4 or 8", nh);
+    ATTNLAB_REQUIRE(key_dtype == ATTNLAB_DT_F16 || key_dtype == ATTNLAB_DT_BF16, "key dtype must be fp16 or bf16");
+    ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= Lk, "need 0 <= lo <= hi <= Lk, got lo=%d hi=%d Lk=%d", lo, hi, Lk);
+    const int M = hi - lo;
+    if (M == 0 || T == 0) return ATTNLAB_OK;
+    ATTNLAB_REQUIRE(keys && q && w && out, "keys, q, w and out are required");
+    ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(keys) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0,
+                    "keys and q must be 16-byte aligned");
+    ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(out) % 16 == 0 && out_stride % 4 == 0 && out_stride >= M,
+                    "out must be 16-byte aligned with a row stride that is a multiple of 4 and >= M=%d (got %lld)", M,
+                    (long long)out_stride);
+    LightningBatchArgs a{keys, q, w, out, out_stride, Lk, T, lo, hi, q_pos0 < 0 ? -1 : q_pos0, relu ? 1 : 0,
+                         (T + kQTile - 1) / kQTile, (M + kKTile - 1) / kKTile};
+    const int64_t blocks = (int64_t)B * KG * a.qtiles * a.ktiles;
+    ATTNLAB_REQUIRE(blocks < (int64_t)1 << 31, "grid of %lld workgroups is too large", (long long)blocks);
+    const dim3 grid((unsigned)blocks), block(256);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool f16 = key_dtype == ATTNLAB_DT_F16;
+#define LAUNCH_LB(NHV)                                                                                        \
+    do {                                                                                                      \
+        if (f16 && relu) hipLaunchKernelGGL((lightning_batched<true, NHV, true>), grid, block, 0, s, a);       \
+        else if (f16) hipLaunchKernelGGL((lightning_batched<true, NHV, false>), grid, block, 0, s, a);         \
+        else if (relu) hipLaunchKernelGGL((lightning_batched<false, NHV, true>), grid, block, 0, s, a);        \
+        else hipLaunchKernelGGL((lightning_batched<false, NHV, false>), grid, block, 0, s, a);                 \
+    } while (0)
+    if (nh == 1) LAUNCH_LB(1);
+    else if (nh == 2) LAUNCH_LB(2);
+    else if (nh == 4) LAUNCH_LB(4);
+    else LAUNCH_LB(8);
+#undef LAUNCH_LB
+    return check_launch("lightning_batched");
+}

@@ -11,6 +11,9 @@ write + u projection + candidate scan, top-k + merge with F, gather-free split-K
 HIP graph and replayed. `value` = batch x steps / elapsed = tokens/s of that path; the same step with the dense decode
 kernel (the A read) is timed beside it. Per-kernel averages come from HIP events around graphs of one kernel type.
 
+`prefill_score` times the batched (prefill) lightning score on the matrix cores beside it: one 8192-token causal
+chunk, 8 index key groups, 4 heads of r = 32, fp16 keys (bench.py's PrefillScore).
+
 The CPU baseline runs the reference's own op sequence (matmul, torch.topk, cat, index_select, SDPA; oracle/ref_path)
 on the host cores for a bounded sample of layer-steps of the same shapes, and is reported, not targeted.
 """
@@ -56,10 +59,17 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 per-layer figures")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the batched (prefill) lightning score figure")
     ap.add_argument("--kernel-reps", type=int, default=20, help="graph replays per kernel-average measurement")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="short run for rocprofv3 --pmc passes: 5 scan launches of one layer at the bench shape, then "
                          "5 plain 256 MiB device copies that calibrate the counters; prints one JSON line")
+    ap.add_argument("--prefill-workload", action="store_true",
+                    help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
+                         "shape; prints one JSON line")
+    ap.add_argument("--prefill-pmc-summary", metavar="DIR",
+                    help="summarise a rocprofv3 --pmc pass of --prefill-workload (SQ_VALU_MFMA_BUSY_CYCLES, "
+                         "GRBM_GUI_ACTIVE, SQ_INSTS_MFMA, SQ_INSTS_VALU) into the matrix-core busy fraction")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise the counter_collection.csv files of a FETCH_SIZE pass and a WRITE_SIZE pass of "
                          "--pmc-workload into HBM bytes per scan launch (no GPU needed)")
@@ -67,6 +77,10 @@ def parse_args():
 
 
 PMC_COPY_BYTES = 256 << 20
+PREFILL_PROFILE = os.path.join(ROOT, "profiles", "lightning_batched_kg8_t8192_pmc.md")
+PREFILL_KERNEL = "lightning_batched"
+PEAK_MFMA_F16_TFLOPS = 2500.0   # dense fp16/bf16 matrix-core peak of MI355X
+MI355X_SIMDS, MI355X_XCDS = 256 * 4, 8
 PMC_PROFILE = os.path.join(ROOT, "profiles", "score_scan_fused_b16_l32k_pmc.md")
 SCAN_KERNEL = "score_scan_fused"
 
@@ -298,6 +312,107 @@ def time_graph(torch, g, reps, warmup):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# batched (prefill) lightning score on the matrix cores
+# ---------------------------------------------------------------------------------------------------------------------
+class PrefillScore:
+    """A prefill chunk of the lightning indexer: T = L = 8192 queries (the C4 prompt length) against their causal
+    prefixes, 8 index key groups (one per KV group), 4 index heads of r = 32, fp16 keys ~ N(0, 1/32), fp32 queries ~
+    N(0, 1), weights ~ U(0, 1), ReLU; fp32 scores of the causal triangle written to [B, KG, T, L]."""
+
+    def __init__(self, torch, dev, *, batch=1, groups=8, tokens=8192, heads=4, seed=0):
+        self.B, self.KG, self.T, self.L, self.nh, self.r = batch, groups, tokens, tokens, heads, 32
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.keys = (torch.randn(batch, groups, tokens, 32, device=dev, generator=gen) / 32 ** 0.5).to(torch.float16)
+        self.q = torch.randn(batch, groups, tokens, heads, 32, device=dev, generator=gen)
+        self.w = torch.rand(batch, groups, tokens, heads, device=dev, generator=gen)
+        self.out = torch.empty(batch, groups, tokens, tokens, device=dev)
+
+    def launch(self):
+        from attention_lab import hip_score
+        hip_score.score_lightning_batched(self.keys, self.q, self.w, 0, self.L, q_pos0=0, out=self.out)
+
+    def scores(self):
+        return self.B * self.KG * self.T * (self.T + 1) // 2
+
+    def algorithmic_bytes(self):
+        """Scores written (4 B each) plus keys, queries and weights read once."""
+        B, KG, T, L, nh, r = self.B, self.KG, self.T, self.L, self.nh, self.r
+        return 4 * self.scores() + B * KG * (L * r * 2 + T * nh * r * 4 + T * nh * 4)
+
+    def flops(self):
+        """Per score: nh dot products of r (2 r flops each), ReLU and the weighted head sum (2 flops per head)."""
+        return self.scores() * self.nh * (2 * self.r + 2)
+
+
+def mfma_busy_from_profile():
+    """Matrix-core busy fraction of the batched score recorded by the committed rocprofv3 --pmc summary, or None."""
+    import re
+    try:
+        with open(PREFILL_PROFILE, encoding="utf-8") as f:
+            m = re.search(r"mfma_busy_frac:\s*([0-9.]+)", f.read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def prefill_pmc_summary(directory):
+    import csv
+    import glob
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    acc = {}
+    for path in files:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if PREFILL_KERNEL in row["Kernel_Name"]:
+                    acc.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    mean = {k: sum(v) / len(v) for k, v in acc.items()}
+    busy, gui = mean["SQ_VALU_MFMA_BUSY_CYCLES"], mean["GRBM_GUI_ACTIVE"]
+    out = {"dispatches": len(acc["GRBM_GUI_ACTIVE"]), "counters_mean_per_dispatch": mean,
+           "cycles_per_xcd": gui / MI355X_XCDS,
+           "mfma_busy_frac": busy / MI355X_SIMDS / (gui / MI355X_XCDS),
+           "mfma_cycles_per_instruction": busy / mean["SQ_INSTS_MFMA"],
+           "valu_instructions_per_mfma": mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"]}
+    print(json.dumps(out, indent=1))
+    return 0
+
+
+def prefill_workload(torch, dev):
+    ps = PrefillScore(torch, dev)
+    for _ in range(5):
+        ps.launch()
+    torch.cuda.synchronize()
+    print(json.dumps({"prefill_workload": f"{PREFILL_KERNEL} x5", "scores": ps.scores(),
+                      "algorithmic_bytes": ps.algorithmic_bytes(), "flops": ps.flops()}))
+    return 0
+
+
+def run_prefill_score(torch, dev, reps=10):
+    ps = PrefillScore(torch, dev)
+    for _ in range(2):
+        ps.launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()   # torch's current stream, which is the stream the op launches on
+    for _ in range(reps):
+        ps.launch()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    gbs = ps.algorithmic_bytes() / (us * 1e-6) / 1e9
+    tflops = ps.flops() / (us * 1e-6) / 1e12
+    res = {"workload": f"B={ps.B}, KG={ps.KG}, T=L={ps.T} causal, nh={ps.nh}, r={ps.r}, fp16 keys, fp32 scores",
+           "avg_launch_us": us, "algorithmic_bytes": ps.algorithmic_bytes(), "gbs": gbs,
+           "hbm_frac": gbs / PEAK_HBM_GBS, "tflops": tflops, "mfma_frac_of_peak": tflops / PEAK_MFMA_F16_TFLOPS,
+           "mfma_busy_frac": mfma_busy_from_profile(), "bound": "hbm (score writes)"}
+    del ps
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # CPU baseline: the reference's op sequence on the host cores
 # ---------------------------------------------------------------------------------------------------------------------
 def cpu_baseline(torch, ls, budget_s, layers_in_step):
@@ -378,6 +493,8 @@ def main() -> int:
     args = parse_args()
     if args.pmc_summary:
         return pmc_summary(*args.pmc_summary)
+    if args.prefill_pmc_summary:
+        return prefill_pmc_summary(args.prefill_pmc_summary)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one GPU, and the "
                                    "multi-GPU design (tensor parallel by KV group) is described in DESIGN.md, not run",
@@ -393,6 +510,8 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     if args.pmc_workload:
         return pmc_workload(torch, dev, args)
+    if args.prefill_workload:
+        return prefill_workload(torch, dev)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,
@@ -471,6 +590,11 @@ def main() -> int:
             line["batch1"] = run_b1(torch, dev, args)
         except Exception as e:  # the headline line must still print
             line["batch1"] = {"error": repr(e)}
+    if not args.no_prefill:
+        try:
+            line["prefill_score"] = run_prefill_score(torch, dev)
+        except Exception as e:  # the headline line must still print
+            line["prefill_score"] = {"error": repr(e)}
 
     if not args.no_cpu_baseline:
         # layer 0 through the fused step once more so ls.rows holds its row list for the numerics comparison

@@ -106,6 +106,20 @@ int attnlab_score_lightning(const uint16_t* keys, int key_dtype, const float* q,
                             void* stream);
 
 /*
+ * Batched (prefill) lightning-indexer score on the matrix cores: the T-query form of attnlab_score_lightning, the
+ * "batched/prefill score contraction" north_star puts on MFMA (no reference kernel; per query it is the formula of
+ * attnlab_score_lightning, and with nh=1, w=1, relu=0 the grouped score of indexer.py:27-29 for T queries):
+ *   out[b,kg,t,m-lo] = sum_i w[b,kg,t,i] * act(sum_j q[b,kg,t,i,j] * key[b,kg,m,j])
+ * for m in [lo, hi) and, when q_pos0 >= 0, m <= q_pos0 + t (causal: query t sits at position q_pos0 + t); entries
+ * past a query's causal bound are not written. keys: [B,KG,Lk,32] fp16/bf16, 16-byte aligned; q: [B,KG,T,nh,32]
+ * fp32, 16-byte aligned; w: [B,KG,T,nh] fp32; out row (b,kg,t) at out + ((b*KG+kg)*T+t)*out_stride, 16-byte aligned,
+ * out_stride a multiple of 4. r must be 32; nh in {1, 2, 4, 8}.
+ */
+int attnlab_score_lightning_batched(const uint16_t* keys, int key_dtype, const float* q, const float* w, float* out,
+                                    int64_t out_stride, int B, int KG, int Lk, int r, int nh, int T, int lo, int hi,
+                                    int q_pos0, int relu, void* stream);
+
+/*
  * Top-k selection with lowest-index tie-break, no reference kernel (the reference calls torch.topk,
  * decode.py:86-93 / :161-166; the planned P2 kernel was never built). For each of R rows of M fp32 scores
  * (row i at scores + i*score_stride) selects the k largest; equal scores resolve to the lower index; NaN ranks below

@@ -10,7 +10,8 @@ Modules (each function cites the reference file:line it restates; paths relative
             metal_score.py:31-40, 84-89), top-k with lowest-index ties (decode.py:86-93 made deterministic), row list
             (decode.py:50-56, 86-93, 160-161), subset attention (metal_attend.py:262-273, reference.py:80-97), dense
             attention (reference.py:51-62, full.py:17-34), causal attention of a prefill chunk (reference.py:28-62,
-            legality mask), lightning score (north_star formula, no reference code)
+            legality mask), lightning score and its T-query prefill form with a causal bound (north_star formula,
+            no reference code)
   ref_path  the reference's torch op sequence on the CPU (matmul -> topk -> cat -> index_select -> SDPA), the timed
             CPU baseline
   weights   GroupedIndexer's seeded weights (indexer.py:38-45)
@@ -23,7 +24,8 @@ How each function is pinned (no function here is "parity unpinned"):
              shift, k0 = capacity sparse == dense, score == the explicit double loop on tiny inputs), brute force
              (top-k against a full sort, including planted ties, NaN and -0.0), and cross-checks of the two
              independent formulations (masked dense vs listed subset; the masked prefill read vs one sliced dense
-             read per query) - tests/test_oracle_pins.py
+             read per query; the batched lightning score vs one single-query score per query, its causal bound
+             element by element) - tests/test_oracle_pins.py
   ref_path   agreement with `exact` on the same inputs (set equality for top-k on tie-free scores) -
              tests/test_oracle_pins.py
   weights    golden fixture written by tests/golden/make_golden.py from the reference's own GroupedIndexer -

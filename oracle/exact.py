@@ -51,6 +51,25 @@ def lightning_scores(keys: np.ndarray, q: np.ndarray, w: np.ndarray, lo: int, hi
     return np.einsum("bki,bkit->bkt", w, dots)
 
 
+def lightning_scores_batched(keys: np.ndarray, q: np.ndarray, w: np.ndarray, lo: int, hi: int, q_pos0=None,
+                             relu: bool = True) -> np.ndarray:
+    """T queries per (b, kg): s[b,kg,t,m-lo] = lightning_scores of query t (q [B,KG,T,nh,r], w [B,KG,T,nh]) for m in
+    [lo, hi); with q_pos0, query t sits at position q_pos0 + t and the entries m > q_pos0 + t are NaN (not scored).
+
+    The prefill form of the north_star lightning indexer (no reference code); one query is lightning_scores.
+    """
+    dots = np.einsum("bktir,bkmr->bktim", q, keys[:, :, lo:hi])
+    if relu:
+        dots = np.maximum(dots, 0.0)
+    s = np.einsum("bkti,bktim->bktm", w, dots)
+    if q_pos0 is not None:
+        T, M = s.shape[2], s.shape[3]
+        m = lo + np.arange(M)[None, :]
+        t = np.arange(T)[:, None]
+        s = np.where(m <= q_pos0 + t, s, np.nan)
+    return s
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # top-k with a defined tie order (decode.py:86-93 made deterministic)
 # ---------------------------------------------------------------------------------------------------------------------

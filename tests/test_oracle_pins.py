@@ -143,6 +143,27 @@ def test_lightning_reduces_to_grouped_and_relu_clamps():
     np.testing.assert_allclose(two, one[0] + one[1])
 
 
+def test_batched_lightning_is_one_single_query_score_per_query_with_a_causal_bound():
+    B, KG, L, r, T, nh, lo, hi, p0 = 2, 2, 40, 32, 5, 2, 3, 37, 20
+    keys = RNG.standard_normal((B, KG, L, r))
+    q = RNG.standard_normal((B, KG, T, nh, r))
+    w = RNG.random((B, KG, T, nh))
+    full = exact.lightning_scores_batched(keys, q, w, lo, hi)
+    causal = exact.lightning_scores_batched(keys, q, w, lo, hi, q_pos0=p0)
+    for t in range(T):
+        one = exact.lightning_scores(keys, q[:, :, t], w[:, :, t], lo, hi)
+        np.testing.assert_allclose(full[:, :, t], one, rtol=1e-12, atol=1e-12)
+        for m in range(lo, hi):   # the causal bound, element by element
+            if m <= p0 + t:
+                np.testing.assert_array_equal(causal[:, :, t, m - lo], full[:, :, t, m - lo])
+            else:
+                assert np.isnan(causal[:, :, t, m - lo]).all()
+    # a unit query on head 0 with weight 1 (others weight 0) and no ReLU reads one key coordinate
+    q1 = np.zeros((1, 1, 1, 1, r)); q1[..., 7] = 1.0
+    s1 = exact.lightning_scores_batched(keys[:1, :1], q1, np.ones((1, 1, 1, 1)), 0, L, relu=False)
+    np.testing.assert_array_equal(s1[0, 0, 0], keys[0, 0, :, 7])
+
+
 # ---------------------------------------------------------------------------------------------------------------------
 # top-k: brute force with planted ties, NaN and signed zeros
 # ---------------------------------------------------------------------------------------------------------------------
