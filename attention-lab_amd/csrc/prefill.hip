@@ -1,4 +1,5 @@
-// Batched (prefill) lightning-indexer scores on the matrix cores of gfx950: T queries of one (b, kg) against its keys,
+// Prefill contractions on the matrix cores of gfx950: the bulk index-table build (project_keys, below) and the batched
+// lightning-indexer score, T queries of one (b, kg) against its keys,
 //   out[b,kg,t,m-lo] = sum_i w[b,kg,t,i] * act(q[b,kg,t,i,:] . key[b,kg,m,:])   m in [lo, hi), m <= q_pos0 + t if causal
 // It is the T-query form of attnlab_score_lightning (one query per (b, kg), HBM-bound, no MFMA). With T queries the
 // contraction over r = 32 is a real GEMM, [T*nh, 32] x [32, M], so it runs on v_mfma_f32_16x16x32_{f16,bf16}; the
@@ -223,10 +224,169 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// Bulk index-table build (prefill): zT[bg, j, col0 + t] = bf16_rne(wk[g, j, :] . k_pre[bg, t, :]) for t < T.
+// Two kernels: project_keys_mfma (d a multiple of 32) and project_keys_lds for other head dims.
+//
+// project_keys_lds: block = 4 waves over 64 positions; lane = position, wave w owns j = w, w + 4, ...; the 64 key rows
+// are staged in LDS (row pitch 136 halves, so lanes reading their own row hit distinct banks) and wk rows are LDS
+// broadcasts. Stores of one j are 64 consecutive columns (128 bytes).
+// ---------------------------------------------------------------------------------------------------------------
+struct ProjectArgs {
+    const uint16_t* k_pre;  // row t of bg at k_pre + bg * k_bg_stride + t * k_row_stride
+    int64_t k_bg_stride, k_row_stride;
+    const uint16_t* wk;     // [G, r, d]
+    uint16_t* zT;           // [BG, r, C]
+    int G, T, r, d, C, col0, tiles;
+    int vec;                // zT columns col0 + 4i are 8-byte aligned (8-byte stores)
+};
+
+constexpr int kProjMaxR = 32;
+constexpr int kProjPos = 64;
+constexpr int kProjPitch = 136;  // halves per staged key row (128 + 8 padding)
+
+__global__ __launch_bounds__(256) void project_keys_lds(ProjectArgs a) {
+    __shared__ uint16_t ks[kProjPos * kProjPitch];
+    __shared__ uint16_t ws[kProjMaxR * 128];
+    const int bg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = tile * kProjPos;
+    // stage 64 key rows (d <= 128 halves each) with 16-byte loads: 16 lanes per row
+    for (int i = tid; i < kProjPos * 16; i += 256) {
+        const int row = i >> 4, seg = i & 15;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (t0 + row < a.T && seg * 8 < a.d)
+            v = *reinterpret_cast<const uint4*>(a.k_pre + (size_t)bg * a.k_bg_stride + (size_t)(t0 + row) * a.k_row_stride + seg * 8);
+        *reinterpret_cast<uint4*>(&ks[row * kProjPitch + seg * 8]) = v;
+    }
+    for (int i = tid; i < a.r * 16; i += 256) {
+        const int j = i >> 4, seg = i & 15;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (seg * 8 < a.d) v = *reinterpret_cast<const uint4*>(a.wk + ((size_t)g * a.r + j) * a.d + seg * 8);
+        *reinterpret_cast<uint4*>(&ws[j * 128 + seg * 8]) = v;
+    }
+    __syncthreads();
+    const int t = t0 + lane;
+    const uint32_t* krow = reinterpret_cast<const uint32_t*>(&ks[lane * kProjPitch]);
+    for (int j = wave; j < a.r; j += 4) {
+        const uint32_t* wrow = reinterpret_cast<const uint32_t*>(&ws[j * 128]);
+        float s = 0.0f;
+        for (int e2 = 0; e2 < a.d / 2; ++e2) {
+            const uint32_t kw = krow[e2], ww = wrow[e2];
+            s += bf16_lo(kw) * bf16_lo(ww);
+            s += bf16_hi(kw) * bf16_hi(ww);
+        }
+        if (t < a.T) a.zT[((size_t)bg * a.r + j) * a.C + a.col0 + t] = f32_to_bf16_rne(s);
+    }
+}
+
+// project_keys_mfma: the GEMM zT[bg, :, cols] = wk[g] (r x d) . k_pre[bg]^T (d x 64) per wave, on
+// v_mfma_f32_16x16x32_bf16 (fp32 accumulate, one RNE to bf16 at the end). A rows are index dims j (two 16-row tiles
+// cover r <= 32); B column n of the c-th of four 16-column tiles is position t0 + 4 n + c, so each lane ends with 4
+// adjacent columns of 8 index dims and writes each dim's 4 columns as one 8-byte store. The wave's 64 key rows are all
+// loaded before the first MFMA. Workgroup = 4 waves = 256 positions of one (b, g).
+template <int KD>   // d / 32
+__global__ __launch_bounds__(256) void project_keys_mfma(ProjectArgs a) {
+    const int bg = blockIdx.x / a.tiles;
+    const int tile = blockIdx.x - bg * a.tiles;
+    const int g = bg % a.G;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, kq = lane >> 4;
+    const int t0 = tile * 256 + wave * 64;
+    if (t0 >= a.T) return;   // whole wave; no barrier in this kernel
+    const uint16_t* kb = a.k_pre + (size_t)bg * a.k_bg_stride + 8 * kq;
+    bf16x8_t kv[4][KD];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int t = min(t0 + 4 * n + c, a.T - 1);   // columns past T compute on row T - 1, not stored
+#pragma unroll
+        for (int kc = 0; kc < KD; ++kc)
+            kv[c][kc] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(kb + (size_t)t * a.k_row_stride + 32 * kc));
+    }
+    bf16x8_t wv[2][KD];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int j = 16 * rt + n;
+        const uint16_t* wr = a.wk + ((size_t)g * a.r + min(j, a.r - 1)) * a.d + 8 * kq;
+#pragma unroll
+        for (int kc = 0; kc < KD; ++kc) {
+            u32x4_t w = *reinterpret_cast<const u32x4_t*>(wr + 32 * kc);
+            if (j >= a.r) w = u32x4_t{0u, 0u, 0u, 0u};
+            wv[rt][kc] = __builtin_bit_cast(bf16x8_t, w);
+        }
+    }
+    f32x4_t acc[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[rt][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kc = 0; kc < KD; ++kc)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+                acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv[rt][kc], kv[c][kc], acc[rt][c], 0, 0, 0);
+    // lane: rows j = 16 rt + 4 kq + i, columns t0 + 4 n + c
+    const int tc = t0 + 4 * n;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 16 * rt + 4 * kq + i;
+            if (j >= a.r) continue;
+            uint16_t h[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) h[c] = f32_to_bf16_rne(acc[rt][c][i]);
+            uint16_t* dst = a.zT + ((size_t)bg * a.r + j) * a.C + a.col0 + tc;
+            if (a.vec && tc + 3 < a.T) {
+                *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{(uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                                            (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (tc + c < a.T) dst[c] = h[c];
+            }
+        }
+    }
+}
+
 }  // namespace
 }  // namespace attnlab
 
 using namespace attnlab;
+
+extern "C" int attnlab_project_keys(const uint16_t* k_pre, int64_t k_bg_stride, int64_t k_row_stride, const uint16_t* wk,
+                                    uint16_t* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && T >= 0, "B=%d G=%d T=%d out of range", B, G, T);
+    ATTNLAB_REQUIRE(r >= 1 && r <= kProjMaxR, "index width r=%d outside [1, %d]", r, kProjMaxR);
+    ATTNLAB_REQUIRE(d >= 2 && d <= 128 && d % 8 == 0, "head_dim d=%d must be a multiple of 8 in [8, 128]", d);
+    ATTNLAB_REQUIRE(0 <= col0 && col0 + T <= C, "columns [%d, %d) outside the table of C=%d", col0, col0 + T, C);
+    ATTNLAB_REQUIRE(k_pre && wk && zT, "k_pre, wk and zT must be device pointers");
+    ATTNLAB_REQUIRE(k_row_stride % 8 == 0 && k_bg_stride % 8 == 0 && reinterpret_cast<uintptr_t>(k_pre) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(wk) % 16 == 0,
+                    "k_pre rows and wk must be 16-byte aligned");
+    if (T == 0) return ATTNLAB_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    ProjectArgs a{k_pre, k_bg_stride, k_row_stride, wk, zT, G, T, r, d, C, col0, 0,
+                  C % 4 == 0 && col0 % 4 == 0 && reinterpret_cast<uintptr_t>(zT) % 8 == 0};
+    if (d % 32 == 0) {
+        a.tiles = (T + 255) / 256;
+        const dim3 grid(B * G * a.tiles), block(256);
+        if (d == 32) hipLaunchKernelGGL(project_keys_mfma<1>, grid, block, 0, s, a);
+        else if (d == 64) hipLaunchKernelGGL(project_keys_mfma<2>, grid, block, 0, s, a);
+        else if (d == 96) hipLaunchKernelGGL(project_keys_mfma<3>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(project_keys_mfma<4>, grid, block, 0, s, a);
+        return check_launch("project_keys_mfma");
+    }
+    a.tiles = (T + kProjPos - 1) / kProjPos;
+    hipLaunchKernelGGL(project_keys_lds, dim3(B * G * a.tiles), dim3(256), 0, s, a);
+    return check_launch("project_keys_lds");
+}
+
 
 extern "C" int attnlab_score_lightning_batched(const uint16_t* keys, int key_dtype, const float* q, const float* w,
                                                float* out, int64_t out_stride, int B, int KG, int Lk, int r, int nh,

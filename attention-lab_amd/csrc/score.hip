@@ -634,79 +634,9 @@ __global__ __launch_bounds__(256) void score_lightning(LightningArgs a) {
     if (ok && quarter == 0) a.out[(size_t)bkg * a.out_stride + (t - a.lo)] = s;
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// Bulk index-table build (prefill): zT[bg, j, col0 + t] = bf16_rne(wk[g, j, :] . k_pre[bg, t, :]) for t < T.
-// Block = 4 waves over 64 positions; lane = position, wave w owns j = w, w + 4, ...; the 64 key rows are staged in
-// LDS (row pitch 136 halves, so lanes reading their own row hit distinct banks) and wk rows are LDS broadcasts.
-// Stores of one j are 64 consecutive columns (128 bytes).
-// ---------------------------------------------------------------------------------------------------------------
-struct ProjectArgs {
-    const uint16_t* k_pre;  // row t of bg at k_pre + bg * k_bg_stride + t * k_row_stride
-    int64_t k_bg_stride, k_row_stride;
-    const uint16_t* wk;     // [G, r, d]
-    uint16_t* zT;           // [BG, r, C]
-    int G, T, r, d, C, col0, tiles;
-};
-
-constexpr int kProjPos = 64;
-constexpr int kProjPitch = 136;  // halves per staged key row (128 + 8 padding)
-
-__global__ __launch_bounds__(256) void project_keys_kernel(ProjectArgs a) {
-    __shared__ uint16_t ks[kProjPos * kProjPitch];
-    __shared__ uint16_t ws[kMaxR * 128];
-    const int bg = blockIdx.x / a.tiles;
-    const int tile = blockIdx.x - bg * a.tiles;
-    const int g = bg % a.G;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = tile * kProjPos;
-    // stage 64 key rows (d <= 128 halves each) with 16-byte loads: 16 lanes per row
-    for (int i = tid; i < kProjPos * 16; i += 256) {
-        const int row = i >> 4, seg = i & 15;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (t0 + row < a.T && seg * 8 < a.d)
-            v = *reinterpret_cast<const uint4*>(a.k_pre + (size_t)bg * a.k_bg_stride + (size_t)(t0 + row) * a.k_row_stride + seg * 8);
-        *reinterpret_cast<uint4*>(&ks[row * kProjPitch + seg * 8]) = v;
-    }
-    for (int i = tid; i < a.r * 16; i += 256) {
-        const int j = i >> 4, seg = i & 15;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (seg * 8 < a.d) v = *reinterpret_cast<const uint4*>(a.wk + ((size_t)g * a.r + j) * a.d + seg * 8);
-        *reinterpret_cast<uint4*>(&ws[j * 128 + seg * 8]) = v;
-    }
-    __syncthreads();
-    const int t = t0 + lane;
-    const uint32_t* krow = reinterpret_cast<const uint32_t*>(&ks[lane * kProjPitch]);
-    for (int j = wave; j < a.r; j += 4) {
-        const uint32_t* wrow = reinterpret_cast<const uint32_t*>(&ws[j * 128]);
-        float s = 0.0f;
-        for (int e2 = 0; e2 < a.d / 2; ++e2) {
-            const uint32_t kw = krow[e2], ww = wrow[e2];
-            s += bf16_lo(kw) * bf16_lo(ww);
-            s += bf16_hi(kw) * bf16_hi(ww);
-        }
-        if (t < a.T) a.zT[((size_t)bg * a.r + j) * a.C + a.col0 + t] = f32_to_bf16_rne(s);
-    }
-}
-
 }  // namespace attnlab
 
 using namespace attnlab;
-
-extern "C" int attnlab_project_keys(const uint16_t* k_pre, int64_t k_bg_stride, int64_t k_row_stride, const uint16_t* wk,
-                                    uint16_t* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream) {
-    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && T >= 0, "B=%d G=%d T=%d out of range", B, G, T);
-    ATTNLAB_REQUIRE(r >= 1 && r <= kMaxR, "index width r=%d outside [1, %d]", r, kMaxR);
-    ATTNLAB_REQUIRE(d >= 2 && d <= 128 && d % 8 == 0, "head_dim d=%d must be a multiple of 8 in [8, 128]", d);
-    ATTNLAB_REQUIRE(0 <= col0 && col0 + T <= C, "columns [%d, %d) outside the table of C=%d", col0, col0 + T, C);
-    ATTNLAB_REQUIRE(k_pre && wk && zT, "k_pre, wk and zT must be device pointers");
-    ATTNLAB_REQUIRE(k_row_stride % 8 == 0 && k_bg_stride % 8 == 0 && reinterpret_cast<uintptr_t>(k_pre) % 16 == 0 &&
-                        reinterpret_cast<uintptr_t>(wk) % 16 == 0,
-                    "k_pre rows and wk must be 16-byte aligned");
-    if (T == 0) return ATTNLAB_OK;
-    ProjectArgs a{k_pre, k_bg_stride, k_row_stride, wk, zT, G, T, r, d, C, col0, (T + kProjPos - 1) / kProjPos};
-    hipLaunchKernelGGL(project_keys_kernel, dim3(B * G * a.tiles), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
-    return check_launch("project_keys");
-}
 
 extern "C" int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                                      const uint16_t* wq_t, const float* u_in, float* u_out, float* out,

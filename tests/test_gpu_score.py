@@ -224,3 +224,24 @@ def test_project_keys_and_chunked_build(gpu):
     torch.cuda.synchronize()
     assert torch.equal(table[..., :C], zT), "chunked build differs from the one-shot build"
     assert bool(torch.isnan(table[..., C:].float()).all()), "columns past the chunk were written"
+
+
+@pytest.mark.parametrize("d,r,C", [(128, 32, 704), (128, 20, 702), (64, 32, 702), (32, 8, 704), (40, 32, 704)])
+def test_project_keys_shapes(gpu, d, r, C):
+    """Matrix-core build (d a multiple of 32) and the LDS build (d = 40): every r, columns that are not 4-aligned
+    (8-byte or 2-byte stores), chunk ends inside a 256-position workgroup, RNE of the exact value."""
+    B, G, T = 2, 3, 700
+    gen = torch.Generator().manual_seed(d + r)
+    k_pre = torch.randn(B, G, C, d, generator=gen).to(torch.bfloat16).to(gpu)
+    wk = (0.02 * torch.randn(G, r, d, generator=gen)).to(torch.bfloat16).to(gpu)
+    ref = exact.project_keys(f64(k_pre[:, :, :T]), f64(wk))
+    bits = bf16.from_f32(ref.astype(np.float32))
+    table = torch.full((B, G, r, C), float("nan"), dtype=torch.bfloat16, device=gpu)
+    bounds = [0, 5, 333, T]
+    for a, b in zip(bounds, bounds[1:]):
+        project_keys(k_pre[:, :, a:b], wk, out=table, col0=a)
+    torch.cuda.synchronize()
+    got = table[..., :T]
+    assert np.mean(bf16.from_torch(got) == bits) >= 0.99
+    assert np.all(np.abs(f64(got) - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6)
+    assert bool(torch.isnan(table[..., T:].float()).all()), "columns past the last chunk were written"
