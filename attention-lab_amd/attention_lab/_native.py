@@ -37,6 +37,7 @@ SIGNATURES = {
     "attnlab_score_lightning": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 8 + [_p]),
     "attnlab_score_lightning_batched": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 10 + [_p]),
     "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
+    "attnlab_topk_tiled": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p, _p, _i64, _p]),
     "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
     "attnlab_select_scratch_bytes": (_i64, [_i, _i]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),

@@ -12,6 +12,8 @@ import torch
 from . import _native as nat
 
 MAX_SCORE_ORDER_K = 4096
+TILED_MIN_M = 32768     # rows at least this long are selected by the tiled kernels (attnlab_topk_tiled)
+TILED_MAX_M = 262144    # ... and at most this long (longer rows take the single-workgroup select)
 ORDERS = {"position": nat.ORDER_POSITION, "score": nat.ORDER_SCORE}
 
 
@@ -21,11 +23,12 @@ def _order_code(order) -> int:
     return ORDERS[order]
 
 
-def topk(scores, k: int, *, order: str = "score"):
+def topk(scores, k: int, *, order: str = "score", tiled=None):
     """Top-k over the last dim of fp32 `scores` [..., M] -> (values fp32 [..., k], indices int64 [..., k]).
 
     order="score": descending score, ties lowest index first (torch.topk's sorted order with ties defined);
-    order="position": the same set, indices ascending.
+    order="position": the same set, indices ascending. tiled: None picks the tiled kernels for rows of
+    TILED_MIN_M..TILED_MAX_M scores, True / False forces the choice (same result either way).
     """
     if scores.dtype != torch.float32 or not scores.is_cuda:
         raise ValueError("scores must be a float32 tensor on a HIP device")
@@ -45,7 +48,15 @@ def topk(scores, k: int, *, order: str = "score"):
     R = s2.shape[0]
     idx = torch.empty(R, max(k, 1), dtype=torch.int32, device=scores.device)
     val = torch.empty(R, max(k, 1), dtype=torch.float32, device=scores.device)
-    if R and k:
+    if tiled is None:
+        tiled = TILED_MIN_M <= M <= TILED_MAX_M
+    if R and k and tiled:
+        state = torch.zeros(R, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=scores.device)
+        nbytes = nat.lib().attnlab_select_scratch_bytes(R, M)
+        scratch = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=scores.device)
+        nat.call("attnlab_topk_tiled", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
+                 idx.stride(0), state.data_ptr(), scratch.data_ptr(), nbytes, nat.stream_of(scores.device))
+    elif R and k:
         nat.call("attnlab_topk", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
                  idx.stride(0), nat.stream_of(scores.device))
     return val[:, :k].reshape(*lead, k), idx[:, :k].long().reshape(*lead, k)
@@ -58,9 +69,9 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
     Returns (rows int32 [B, G, S] original positions, flat int64 [B*G*S] row ids of the flattened cache or None),
     S = lo + (legal - hi) + k. order="position" sorts every list ascending (canonical_order); order="score" puts F
     first and then the candidates by descending score, like cat(fixed_rows, topk.indices) in decode.py:93.
-    state: the select state score_grouped(..., state=) filled for these scores (cleared here), or None. With a state,
-    position order and tiled=True the keys are classified by a grid of 4096-key tiles and each row resolved by one
-    workgroup (same result as the single-workgroup select).
+    state: the select state score_grouped(..., state=) filled for these scores (cleared here), or None. With a state
+    and tiled=True the keys are classified by a grid of 4096-key tiles and each row resolved by one workgroup (same
+    result as the single-workgroup select, in either order).
     """
     if scores.dim() != 3 or scores.dtype != torch.float32 or not scores.is_cuda or scores.stride(2) != 1:
         raise ValueError("scores must be a float32 [B, G, M] tensor with unit column stride on a HIP device")
@@ -88,7 +99,7 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
                               or not state.is_contiguous() or state.device != scores.device):
         raise ValueError(f"state must be a contiguous int32 [{B}, {G}, {W}] tensor on the scores' device")
     scratch = None
-    if state is not None and tiled and code == nat.ORDER_POSITION and k > 0:
+    if state is not None and tiled and k > 0:
         nbytes = nat.lib().attnlab_select_scratch_bytes(B * G, M)
         scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=scores.device)
     nat.call("attnlab_select_rows", scores.data_ptr(), stride, B, G, lo, hi, legal, k, capacity, code,

@@ -9,8 +9,10 @@
 //
 // Lightning mode (the north_star generalisation; no reference kernel): keys are stored one r-vector per position
 // [B,KG,Lk,r] (64 bytes of fp16/bf16 per position), four lanes share a position with 16 bytes each, the per-head
-// partial dot products are finished with two DPP quad steps, and ReLU and the head weights are applied in fp32.
+// partial dot products of a quad's four keys are reduced and transposed with two DPP steps, and ReLU and the head
+// weights are applied in fp32.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "select.h"
@@ -144,37 +146,6 @@ __device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
         s = sum8(s);
         if ((tid & 7) == 0 && j < a.r) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = f32_to_bf16_rne(s);
     }
-}
-
-// First-digit histogram of this block's scores (the select kernel's first radix pass), flushed to the row's global
-// histogram with one device atomic per non-empty bin. Called by every thread of the block.
-template <int BLOCK>
-__device__ __forceinline__ void flush_histogram(uint32_t* hsh, uint32_t* ghist, int bg) {
-    static_assert(BLOCK >= kSuperBins, "one thread per super-bin");
-    __syncthreads();
-    uint32_t* row = ghist + (size_t)bg * kSelectStateWords;
-    // bins: thread t -> t, t + BLOCK, ...: the lanes of one atomic instruction hit consecutive words (two lines)
-    for (int b = threadIdx.x; b < kHistBins; b += BLOCK) {
-        const uint32_t c = hsh[b];
-        if (c) atomicAdd(row + b, c);
-    }
-    // super-bins: lane s of the first wave sums bins [32 s, 32 s + 32), starting at a lane-dependent chunk so the
-    // lanes spread over the LDS banks
-    if (threadIdx.x < kSuperBins) {
-        const int sb = threadIdx.x;
-        uint32_t sum = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint4 v = *reinterpret_cast<const uint4*>(hsh + 32 * sb + 4 * ((sb + j) & 7));
-            sum += v.x + v.y + v.z + v.w;
-        }
-        if (sum) atomicAdd(row + kHistBins + sb, sum);
-    }
-}
-
-template <int BLOCK>
-__device__ __forceinline__ void clear_histogram(uint32_t* hsh) {
-    for (int b = threadIdx.x; b < kHistBins; b += BLOCK) hsh[b] = 0u;
 }
 
 // 8-byte-load scan: thread -> 4 adjacent columns starting at a 4-aligned column, 32 non-temporal 8-byte loads (the
@@ -579,7 +550,7 @@ static void launch_prologue(const ScoreArgs& a, int BG, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Lightning mode. Block = 256 threads = 64 positions (4 lanes x 16 bytes each); q and w are staged in LDS.
+// Lightning mode: keys one 32-vector per position, nh index heads, ReLU and per-head weights (see score_lightning).
 // ---------------------------------------------------------------------------------------------------------------
 struct LightningArgs {
     const uint16_t* keys;  // [BKG, Lk, 32]
@@ -587,51 +558,160 @@ struct LightningArgs {
     const float* w;        // [BKG, nh]
     float* out;
     int64_t out_stride;
-    int Lk, nh, lo, M, relu, tiles;
+    int Lk, nh, lo, M;
+    int tiles;             // tiles per row; a tile is 256 * ng keys
+    int ng;                // 64-key groups per wave per tile
 };
 
-template <bool F16, int NH>
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// a.x * b.x + a.y * b.y + c on packed 16-bit pairs, fp32 accumulate (v_dot2_f32_f16 / v_dot2_f32_bf16)
+template <bool F16>
+__device__ __forceinline__ float dot2_16(uint32_t a, uint32_t b, float c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+    else
+        return dot2_bf16(a, b, c);
+}
+
+// (x, y) -> packed 16-bit pair (RNE) and its value back in fp32
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2_16(float x, float y, float& xr, float& yr) {
+    if constexpr (F16) {
+        const f16x2_t h = {(_Float16)x, (_Float16)y};
+        xr = (float)h.x;
+        yr = (float)h.y;
+        return __builtin_bit_cast(uint32_t, h);
+    } else {
+        const uint32_t lo16 = f32_to_bf16_rne(x), hi16 = f32_to_bf16_rne(y);
+        xr = bf16_to_f32((uint16_t)lo16);
+        yr = bf16_to_f32((uint16_t)hi16);
+        return lo16 | (hi16 << 16);
+    }
+}
+
+__device__ __forceinline__ float relu_f32(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
+// Lightning-indexer score, one query per (b, kg) (decode):
+//   out[bkg, m] = sum_i w[bkg, i] * act(q[bkg, i, :] . key[bkg, lo + m, :])
+// HBM-bound: 64 key bytes in, 4 score bytes out per position. Lane (quad qd, quarter c) reads dims [8c, 8c + 8) of a
+// key with one 16-byte load, so each load instruction covers 16 whole keys = 1 KiB contiguous; a wave takes 64 keys
+// per group (four loads per lane), double-buffered, and the four waves of a workgroup read adjacent 4 KiB chunks.
+// With fp16 keys the fp32 query is held as fp16 head + remainder pairs (q = hi + lo) and multiplied with v_dot2_f32_f16
+// (fp32 accumulate); with bf16 keys the keys are widened to fp32. Either way scores keep fp32 accuracy. The quad's partial sums of its 4 keys are reduced and transposed with two
+// DPP steps (xor 1, xor 2), after which lane c holds all heads of key c; ReLU and the head weights follow, and the
+// wave's 64 scores go out as one 256-byte store.
+template <bool F16, int NH, bool RELU>
 __global__ __launch_bounds__(256) void score_lightning(LightningArgs a) {
-    __shared__ float q_sh[NH][32];
-    __shared__ float w_sh[NH];
-    const int bkg = blockIdx.x / a.tiles;
-    const int tile = blockIdx.x - bkg * a.tiles;
-    const int tid = threadIdx.x;
-    const int quarter = tid & 3;                  // dims [8*quarter, 8*quarter + 8)
-    const int t = a.lo + tile * 64 + (tid >> 2);  // position
-    const bool ok = t < a.lo + a.M;
-    uint4 kv = make_uint4(0, 0, 0, 0);
-    if (ok) kv = *reinterpret_cast<const uint4*>(a.keys + ((size_t)bkg * a.Lk + t) * 32 + quarter * 8);
-    if (tid < NH * 32) {
-        const int i = tid >> 5;
-        q_sh[i][tid & 31] = i < a.nh ? a.q[((size_t)bkg * a.nh + i) * 32 + (tid & 31)] : 0.0f;
-    }
-    if (tid < NH) w_sh[tid] = tid < a.nh ? a.w[(size_t)bkg * a.nh + tid] : 0.0f;
-    __syncthreads();
-    float kf[8];
-    const uint32_t words[4] = {kv.x, kv.y, kv.z, kv.w};
+    const int lin = xcd_contiguous_block();
+    const int bkg = lin / a.tiles, tile = lin - bkg * a.tiles;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int qd = lane >> 2, c = lane & 3;
+    // fp16 keys: q as 16-bit head + remainder pairs for v_dot2_f32_f16 (remainder error ~2^-22 |q|); bf16 keys: q in
+    // fp32 and the keys widened (exact), since a bf16 head + remainder keeps only ~17 bits of q
+    uint32_t qh[NH][4], ql[NH][4];
+    float qf[F16 ? 1 : NH][8];
+    float w[NH];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (F16) {
-            kf[2 * i] = f16_to_f32((uint16_t)(words[i] & 0xffffu));
-            kf[2 * i + 1] = f16_to_f32((uint16_t)(words[i] >> 16));
+    for (int h = 0; h < NH; ++h) {
+        const int hh = min(h, a.nh - 1);
+        const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)bkg * a.nh + hh) * 32 + 8 * c);
+        const float4 x0 = qp[0], x1 = qp[1];
+        const bool on = h < a.nh;
+        const float x[8] = {on ? x0.x : 0.0f, on ? x0.y : 0.0f, on ? x0.z : 0.0f, on ? x0.w : 0.0f,
+                            on ? x1.x : 0.0f, on ? x1.y : 0.0f, on ? x1.z : 0.0f, on ? x1.w : 0.0f};
+        if constexpr (F16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float xr, yr, d0, d1;
+                qh[h][i] = pack2_16<F16>(x[2 * i], x[2 * i + 1], xr, yr);
+                ql[h][i] = pack2_16<F16>(x[2 * i] - xr, x[2 * i + 1] - yr, d0, d1);
+            }
         } else {
-            kf[2 * i] = bf16_lo(words[i]);
-            kf[2 * i + 1] = bf16_hi(words[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[h][e] = x[e];
         }
+        w[h] = on ? a.w[(size_t)bkg * a.nh + hh] : 0.0f;
     }
-    float s = 0.0f;
+    const uint16_t* kb = a.keys + ((size_t)bkg * a.Lk + a.lo) * 32 + 8 * c;
+    float* orow = a.out + (size_t)bkg * a.out_stride;
+    const int tile_base = tile * 256 * a.ng;
+    // group g of this wave: keys tile_base + 64 (4 g + wave) + [0, 64); load jj: key + 16 jj + qd (clamped: past the
+    // end a real key is read and its score not stored)
+    auto load = [&](int g, u32x4_t (&b)[4]) {
+        const int gbase = tile_base + 64 * (4 * g + wave);
 #pragma unroll
-    for (int i = 0; i < NH; ++i) {
-        float dsum = 0.0f;
+        for (int jj = 0; jj < 4; ++jj) {
+            const int m = min(gbase + 16 * jj + qd, a.M - 1);
+            b[jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kb + (size_t)m * 32));
+        }
+    };
+    auto process = [&](int g, const u32x4_t (&b)[4], bool masked) {
+        float p[NH][4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dsum += q_sh[i][quarter * 8 + e] * kf[e];
-        dsum += dpp_f32<0xB1>(dsum);
-        dsum += dpp_f32<0x4E>(dsum);
-        if (a.relu) dsum = fmaxf(dsum, 0.0f);
-        s += w_sh[i] * dsum;
-    }
-    if (ok && quarter == 0) a.out[(size_t)bkg * a.out_stride + (t - a.lo)] = s;
+        for (int jj = 0; jj < 4; ++jj) {
+            const uint32_t kw[4] = {b[jj].x, b[jj].y, b[jj].z, b[jj].w};
+            if constexpr (F16) {
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s = dot2_16<F16>(kw[i], qh[h][i], s);
+                        s = dot2_16<F16>(kw[i], ql[h][i], s);
+                    }
+                    p[h][jj] = s;
+                }
+            } else {
+                float kf[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kf[2 * i] = bf16_lo(kw[i]);
+                    kf[2 * i + 1] = bf16_hi(kw[i]);
+                }
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s += qf[h][e] * kf[e];
+                    p[h][jj] = s;
+                }
+            }
+        }
+        const bool b0 = (c & 1) != 0, b1 = (c & 2) != 0;
+        float score = 0.0f;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            float r[2];
+#pragma unroll
+            for (int m2 = 0; m2 < 2; ++m2) {   // xor 1: keep the keys whose bit 0 matches this lane's
+                const float keep = b0 ? p[h][2 * m2 + 1] : p[h][2 * m2];
+                const float send = b0 ? p[h][2 * m2] : p[h][2 * m2 + 1];
+                r[m2] = keep + dpp_f32<0xB1>(send);
+            }
+            const float keep = b1 ? r[1] : r[0];   // xor 2: keep key c
+            const float send = b1 ? r[0] : r[1];
+            const float s = keep + dpp_f32<0x4E>(send);
+            score += w[h] * (RELU ? relu_f32(s) : s);
+        }
+        const int m = tile_base + 64 * (4 * g + wave) + 16 * c + qd;
+        if (!masked || m < a.M) orow[m] = score;
+    };
+    auto run = [&](auto masked_tag) {
+        constexpr bool kMasked = decltype(masked_tag)::value;
+        u32x4_t A[4], B[4];
+        load(0, A);
+        int g = 0;
+        for (; g + 2 <= a.ng; g += 2) {
+            load(g + 1, B);
+            process(g, A, kMasked);
+            load(g + 2, A);
+            process(g + 1, B, kMasked);
+        }
+        if (g < a.ng) process(g, A, kMasked);
+    };
+    if (tile_base + 256 * a.ng > a.M) run(std::true_type{});   // the row's last, partial tile
+    else run(std::false_type{});
 }
 
 }  // namespace attnlab
@@ -742,14 +822,22 @@ extern "C" int attnlab_score_lightning(const uint16_t* keys, int key_dtype, cons
     const int M = hi - lo;
     if (M == 0) return ATTNLAB_OK;
     ATTNLAB_REQUIRE(out != nullptr && out_stride >= M, "out must hold M=%d scores per row", M);
-    LightningArgs a{keys, q, w, out, out_stride, Lk, nh, lo, M, relu, (M + 63) / 64};
-    const dim3 grid(B * KG * a.tiles);
+    ATTNLAB_REQUIRE(q != nullptr && w != nullptr && reinterpret_cast<uintptr_t>(q) % 16 == 0,
+                    "q and w are required; q must be 16-byte aligned");
+    // 64-key groups per wave and tile: tiles of 256..2048 keys, as large as still gives ~1024 workgroups
+    const int64_t per = (int64_t)M * B * KG / 262144;
+    const int ng = (int)std::min<int64_t>(8, std::max<int64_t>(1, per));
+    const int tiles = (M + 256 * ng - 1) / (256 * ng);
+    LightningArgs a{keys, q, w, out, out_stride, Lk, nh, lo, M, tiles, ng};
+    const dim3 grid(B * KG * tiles);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = key_dtype == ATTNLAB_DT_F16;
-#define LAUNCH_LIGHTNING(NHV)                                                                           \
-    do {                                                                                                \
-        if (f16) hipLaunchKernelGGL((score_lightning<true, NHV>), grid, dim3(256), 0, s, a);           \
-        else hipLaunchKernelGGL((score_lightning<false, NHV>), grid, dim3(256), 0, s, a);              \
+#define LAUNCH_LIGHTNING(NHV)                                                                                      \
+    do {                                                                                                           \
+        if (f16 && relu) hipLaunchKernelGGL((score_lightning<true, NHV, true>), grid, dim3(256), 0, s, a);         \
+        else if (f16) hipLaunchKernelGGL((score_lightning<true, NHV, false>), grid, dim3(256), 0, s, a);           \
+        else if (relu) hipLaunchKernelGGL((score_lightning<false, NHV, true>), grid, dim3(256), 0, s, a);          \
+        else hipLaunchKernelGGL((score_lightning<false, NHV, false>), grid, dim3(256), 0, s, a);                   \
     } while (0)
     if (nh <= 1) LAUNCH_LIGHTNING(1);
     else if (nh <= 2) LAUNCH_LIGHTNING(2);

@@ -24,6 +24,37 @@ __device__ __forceinline__ uint32_t score_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// First-digit histogram of this block's scores (the select kernel's first radix pass), flushed to the row's global
+// histogram with one device atomic per non-empty bin. Called by every thread of the block.
+template <int BLOCK>
+__device__ __forceinline__ void flush_histogram(uint32_t* hsh, uint32_t* ghist, int bg) {
+    static_assert(BLOCK >= kSuperBins, "one thread per super-bin");
+    __syncthreads();
+    uint32_t* row = ghist + (size_t)bg * kSelectStateWords;
+    // bins: thread t -> t, t + BLOCK, ...: the lanes of one atomic instruction hit consecutive words (two lines)
+    for (int b = threadIdx.x; b < kHistBins; b += BLOCK) {
+        const uint32_t c = hsh[b];
+        if (c) atomicAdd(row + b, c);
+    }
+    // super-bins: lane s of the first wave sums bins [32 s, 32 s + 32), starting at a lane-dependent chunk so the
+    // lanes spread over the LDS banks
+    if (threadIdx.x < kSuperBins) {
+        const int sb = threadIdx.x;
+        uint32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hsh + 32 * sb + 4 * ((sb + j) & 7));
+            sum += v.x + v.y + v.z + v.w;
+        }
+        if (sum) atomicAdd(row + kHistBins + sb, sum);
+    }
+}
+
+template <int BLOCK>
+__device__ __forceinline__ void clear_histogram(uint32_t* hsh) {
+    for (int b = threadIdx.x; b < kHistBins; b += BLOCK) hsh[b] = 0u;
+}
+
 // attnlab_select_rows: `state` [B*G][kSelectStateWords] (nullable) holds the first-digit histograms the score kernel
 // built; with it and a scratch of select_scratch_bytes(B*G, M) the position-order select runs tiled over the chip.
 int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,

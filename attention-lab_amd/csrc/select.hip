@@ -401,22 +401,24 @@ static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Tiled select (position order, first-digit histogram given), two launches:
+// Tiled select (first-digit histogram given by the score kernel, or built by select_hist for attnlab_topk_tiled):
 //   A select_classify  (rows x tiles of 4096 keys, 256 threads): the threshold's first digit b1 from the row's
 //                      super-bins and bins; every key of the tile is classified as "above" (first digit > b1: selected for sure)
 //                      or "candidate" (first digit == b1), written as two bitmaps of the row (one bit per key).
 //   B select_resolve   (one 1024-thread workgroup per row): compacts the candidate bitmap into an index-ordered list,
 //                      gathers the candidates' scores, finds the threshold among them with the remaining two radix
 //                      digits, takes the tied keys at the threshold in index order, ORs the selected candidates into
-//                      the "above" bitmap in LDS and writes the set bits in index order (plus F); it then clears the
-//                      row's histogram. A row with more than kCandCap candidates runs the single-workgroup select.
+//                      the "above" bitmap in LDS and writes the set bits in index order (plus F), or in score order
+//                      after one LDS sort; it then clears the row's histogram. A row with more than kCandCap candidates
+//                      runs the single-workgroup select.
 // Every kernel issues its global loads before it uses any of them: each is a few memory round trips long.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int kTileKeys = 4096;
 constexpr int kTileThreads = 256;
 constexpr int kTileKPT = kTileKeys / kTileThreads;   // 16 keys per thread, one contiguous segment (half a bitmap word)
-constexpr int kCandCap = 4096;                        // candidates per row, listed in LDS
+constexpr int kCandCap = 8192;                        // candidates per row, listed in LDS (in sortbuf)
 constexpr int kCandPerThread = kCandCap / kSelThreads;
+static_assert(kCandCap * sizeof(uint32_t) <= sizeof(SelectShared::sortbuf), "the candidate list lives in sortbuf");
 constexpr int kMaxWords = 8192;                       // bitmap words per row held in LDS: M <= 262144
 constexpr int kMaxWordsPerThread = kMaxWords / kSelThreads;
 
@@ -497,6 +499,23 @@ __global__ __launch_bounds__(kTileThreads) void select_classify(SelectArgs a, Ti
         t.above[(size_t)row * t.W + w] = abits | (an << 16);
         t.cand[(size_t)row * t.W + w] = cbits | (cn << 16);
     }
+}
+
+// Standalone top-k (no score kernel in front): the first-digit histogram and super-bin counts of every row, over the
+// same 4096-key tiles, added into the row's select state.
+__global__ __launch_bounds__(kTileThreads) void select_hist(SelectArgs a, TiledArgs t) {
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
+    const int lin = xcd_contiguous_block();
+    const int row = lin / t.T, tile = lin - row * t.T;
+    const int tid = threadIdx.x;
+    float v[kTileKPT];
+    const int nvalid = load_tile_scores(a.scores + (size_t)row * a.score_stride, tile * kTileKeys + tid * kTileKPT, a.M, v);
+    clear_histogram<kTileThreads>(hsh);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTileKPT; ++i)
+        if (i < nvalid) atomicAdd(&hsh[score_key(v[i]) >> kHistShift], 1u);
+    flush_histogram<kTileThreads>(hsh, a.hist, row);
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, TiledArgs t) {
@@ -598,7 +617,9 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
         }
     }
     __syncthreads();
-    // emission: the set bits of this thread's words, in index order
+    // emission: the set bits of this thread's words, in index order; in score order they are staged as (key, ~index)
+    // pairs in sortbuf (the candidate list there was consumed before the last barrier) and finish_row sorts them
+    init_sortbuf(a, sh);
     uint32_t sw[kMaxWordsPerThread];
     uint32_t ns = 0;
 #pragma unroll
@@ -608,10 +629,8 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     }
     uint32_t slot, unused3, tsel, unused_t3;
     block_scan2<kSelThreads>(ns, 0u, slot, unused3, tsel, unused_t3, sh.wave_tot);
-    const int nrec = a.legal - a.hi, S = a.lo + nrec + a.k, nf = a.lo + nrec;
-    int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride : nullptr;
-    int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S : nullptr;
-    const int64_t base = (int64_t)row * a.C;
+    const Emitter em = make_emitter(a, row, sh);
+    const bool by_score = a.order == ATTNLAB_ORDER_SCORE;
 #pragma unroll
     for (int j = 0; j < kMaxWordsPerThread; ++j) {
         uint32_t word = sw[j];
@@ -619,24 +638,17 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
             const uint32_t b = __ffs(word) - 1;
             word &= word - 1;
             const int idx = (w0 + j) * 32 + (int)b;
-            if (slot < (uint32_t)a.k) {
-                if (rows) rows[a.lo + slot] = a.lo + idx;
-                if (flat) flat[a.lo + slot] = base + a.lo + idx;
-            }
-            ++slot;
+            em.put(slot++, idx, by_score ? score_key(srow[idx]) : 0u);
         }
-    }
-    for (int f = tid; f < nf; f += kSelThreads) {
-        const int p = f < a.lo ? f : a.hi + (f - a.lo);
-        const int s_out = f < a.lo ? f : a.lo + a.k + (f - a.lo);
-        if (rows) rows[s_out] = p;
-        if (flat) flat[s_out] = base + p;
     }
     uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
     for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
+    __syncthreads();
+    finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
 }
 
-static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s) {
+static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s, bool build_hist = false) {
+    if (build_hist) hipLaunchKernelGGL(select_hist, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
     hipLaunchKernelGGL(select_classify, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
     hipLaunchKernelGGL(select_resolve, dim3(R), dim3(kSelThreads), 0, s, a, t);
     return check_launch("select_tiled");
@@ -665,7 +677,7 @@ int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, in
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
     const int W = (M + 31) / 32;
-    const bool tiled = state && scratch && k > 0 && order == ATTNLAB_ORDER_POSITION && W <= kMaxWords &&
+    const bool tiled = state && scratch && k > 0 && W <= kMaxWords &&
                        (reinterpret_cast<uintptr_t>(state) & 15) == 0 && (reinterpret_cast<uintptr_t>(scratch) & 3) == 0 &&
                        scratch_bytes >= tiled_scratch_bytes(R, M);
     if (!tiled) return launch_select(a, R, stream);
@@ -694,6 +706,39 @@ extern "C" int attnlab_topk(const float* scores, int64_t score_stride, int R, in
     SelectArgs a{scores, score_stride, M, k, 0, 0, 0, 1, 0, order, nullptr, 0, nullptr, top_idx, top_val, top_stride,
                  nullptr};
     return launch_select(a, R, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, int k, int order,
+                                  int32_t* top_idx, float* top_val, int64_t top_stride, uint32_t* state, void* scratch,
+                                  int64_t scratch_bytes, void* stream) {
+    ATTNLAB_REQUIRE(R >= 0 && M >= 0, "R=%d and M=%d must be non-negative", R, M);
+    ATTNLAB_REQUIRE(0 <= k && k <= M, "need 0 <= k <= M, got k=%d M=%d", k, M);
+    ATTNLAB_REQUIRE(order == ATTNLAB_ORDER_POSITION || order == ATTNLAB_ORDER_SCORE, "unknown order %d", order);
+    ATTNLAB_REQUIRE(order != ATTNLAB_ORDER_SCORE || k <= kMaxScoreOrderK, "score order supports k <= %d, got %d",
+                    kMaxScoreOrderK, k);
+    if (R == 0 || k == 0) return ATTNLAB_OK;
+    ATTNLAB_REQUIRE(scores != nullptr && score_stride >= M, "scores must hold M=%d values per row", M);
+    ATTNLAB_REQUIRE(top_stride >= k, "top_stride=%lld smaller than k=%d", (long long)top_stride, k);
+    const int W = (M + 31) / 32;
+    ATTNLAB_REQUIRE(state != nullptr && (reinterpret_cast<uintptr_t>(state) & 15) == 0,
+                    "state must be a 16-byte aligned [R, %d] buffer", kSelectStateWords);
+    ATTNLAB_REQUIRE(scratch != nullptr && (reinterpret_cast<uintptr_t>(scratch) & 3) == 0 &&
+                        scratch_bytes >= tiled_scratch_bytes(R, M),
+                    "scratch must hold attnlab_select_scratch_bytes(%d, %d) = %lld bytes", R, M,
+                    (long long)tiled_scratch_bytes(R, M));
+    SelectArgs a{scores, score_stride, M, k, 0, 0, 0, 1, 0, order, nullptr, 0, nullptr, top_idx, top_val, top_stride,
+                 state};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (W > kMaxWords) {   // rows past 262144 keys: single-workgroup select, which builds its own histograms
+        a.hist = nullptr;
+        return launch_select(a, R, s);
+    }
+    TiledArgs t;
+    t.above = static_cast<uint32_t*>(scratch);
+    t.cand = t.above + (size_t)R * W;
+    t.W = W;
+    t.T = (M + kTileKeys - 1) / kTileKeys;
+    return launch_tiled(a, t, R, s, true);
 }
 
 extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal,

@@ -64,6 +64,9 @@ def parse_args():
     ap.add_argument("--pmc-workload", action="store_true",
                     help="short run for rocprofv3 --pmc passes: 5 scan launches of one layer at the bench shape, then "
                          "5 plain 256 MiB device copies that calibrate the counters; prints one JSON line")
+    ap.add_argument("--sweeps", nargs="?", const="all", choices=("all", "score", "attend"),
+                    help="instead of the bench line: the microbenchmark sweeps of BASELINE configs[1] (lightning score "
+                         "+ top-k) and configs[2] (gather-free attend vs dense), one JSON line per case")
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
@@ -413,6 +416,156 @@ def run_prefill_score(torch, dev, reps=10):
 
 
 # ---------------------------------------------------------------------------------------------------------------------
+# microbenchmark sweeps of configs[1] and configs[2]
+# ---------------------------------------------------------------------------------------------------------------------
+COLD_BYTES = 1 << 30   # rotate over input copies of at least this many bytes, so reads come from HBM, not the caches
+
+
+def time_rotating(torch, launch, copies, reps=10):
+    """launch(i) runs one kernel on copy i; one graph launches every copy once; returns µs per launch."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(copies):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(copies):
+            launch(i)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * copies)
+
+
+def sweep_lightning_topk(torch, dev, emit):
+    """batch {1, 8, 32} x L {4K, 16K, 64K, 128K}, 4 index heads of r = 32, fp16 keys ~ N(0, 1/32),
+    q ~ N(0, 1), w ~ U(0, 1), ReLU, k = L / 32; 2 % of each row's positions get +3 sigma of that row's scores before
+    the top-k. Key groups G_I = 1 (one shared index per sequence) and 8 (one per KV group)."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_select
+    for KG in (1, 8):
+        for B in (1, 8, 32):
+            for L in (4096, 16384, 65536, 131072):
+                nh, k = 4, L // 32
+                gen = torch.Generator(device=dev)
+                gen.manual_seed(B * L + KG)
+                per = B * KG * L * 64
+                copies = max(2, min(16, -(-COLD_BYTES // per)))
+                keys = [(torch.randn(B, KG, L, 32, device=dev, generator=gen) / 32 ** 0.5).to(torch.float16)
+                        for _ in range(copies)]
+                q = torch.randn(B, KG, nh, 32, device=dev, generator=gen)
+                w = torch.rand(B, KG, nh, device=dev, generator=gen)
+                sc = [torch.empty(B * KG, L, device=dev) for _ in range(copies)]
+                stream = lambda: torch.cuda.current_stream(dev).cuda_stream
+
+                def score(i):
+                    nat.call("attnlab_score_lightning", keys[i].data_ptr(), nat.DT_F16, q.data_ptr(), w.data_ptr(),
+                             sc[i].data_ptr(), L, B, KG, L, 32, nh, 0, L, 1, stream())
+                us_score = time_rotating(torch, score, copies)
+                for i in range(copies):   # heavy tail: +3 sigma on 2 % of each row's positions
+                    mask = torch.rand(B * KG, L, device=dev, generator=gen) < 0.02
+                    sc[i] += mask * (3.0 * sc[i].std(dim=1, keepdim=True))
+                idx = torch.empty(B * KG, k, dtype=torch.int32, device=dev)
+                val = torch.empty(B * KG, k, device=dev)
+                # the selection hip_select.topk runs for these rows: tiled over the chip for 8K..256K scores (state
+                # zeroed once, left zeroed by every call), one workgroup per row below
+                state = torch.zeros(B * KG, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
+                nbytes = nat.lib().attnlab_select_scratch_bytes(B * KG, L)
+                scratch = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
+                tiled = hip_select.TILED_MIN_M <= L <= hip_select.TILED_MAX_M
+
+                def select(i):
+                    if tiled:
+                        nat.call("attnlab_topk_tiled", sc[i].data_ptr(), L, B * KG, L, k, nat.ORDER_SCORE,
+                                 idx.data_ptr(), val.data_ptr(), k, state.data_ptr(), scratch.data_ptr(), nbytes,
+                                 stream())
+                    else:
+                        nat.call("attnlab_topk", sc[i].data_ptr(), L, B * KG, L, k, nat.ORDER_SCORE, idx.data_ptr(),
+                                 val.data_ptr(), k, stream())
+                us_topk = time_rotating(torch, select, copies)
+                score_bytes = B * KG * (L * 64 + L * 4) + B * KG * nh * (32 * 4 + 4)
+                topk_bytes = B * KG * (4 * L + 8 * k)
+                emit({"sweep": "lightning_score_topk", "batch": B, "key_groups": KG, "L": L, "k": k,
+                      "topk_kernels": "tiled (histogram, classify, resolve)" if tiled else "one workgroup per row",
+                      "score_us": us_score, "score_gbs": score_bytes / us_score / 1e3,
+                      "score_frac": score_bytes / us_score / 1e3 / PEAK_HBM_GBS,
+                      "topk_us": us_topk, "topk_gbs": topk_bytes / us_topk / 1e3})
+                del keys, sc
+                torch.cuda.empty_cache()
+
+
+def sweep_attend(torch, dev, emit):
+    """L = 32K, 8 KV groups x 2 query heads, d = 128, bf16 K/V ~ N(0, 1); rows = 4 sinks + the 128 most
+    recent positions + k uniform picks from the rest (S = 132 + k), k in {64, 256, 1024, 2048}, batch {1, 16}, rows
+    sorted and unsorted; against the dense decode kernel at the same shape."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_attend
+    L, G, h, d = 32768, 8, 2, 128
+    for B in (1, 16):
+        per = B * G * L * d * 2 * 2
+        copies = max(2, min(16, -(-COLD_BYTES // per)))
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(B)
+        K = [torch.randn(B, G, L, d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(copies)]
+        V = [torch.randn(B, G, L, d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(copies)]
+        q = torch.randn(B, G, h, d, device=dev, generator=gen, dtype=torch.bfloat16)
+        out = torch.empty(B, G, h, d, device=dev, dtype=torch.bfloat16)
+        stream = lambda: torch.cuda.current_stream(dev).cuda_stream
+        BG = B * G
+        Pd = hip_attend.dense_partitions(BG, L)
+        part = torch.empty(BG * max(64, Pd) * h * 130, device=dev)
+
+        def dense(i):
+            nat.call("attnlab_dense_decode", K[i].data_ptr(), V[i].data_ptr(), L * d, d, q.data_ptr(), B, G, h, L, L,
+                     Pd, 1.0 / math.sqrt(d), out.data_ptr(), 1, part.data_ptr(), stream())
+        us_dense = time_rotating(torch, dense, copies)
+        for k in (64, 256, 1024, 2048):
+            S = 132 + k
+            P = hip_attend.sparse_partitions(BG, S, h)
+            base = torch.cat([torch.arange(4, device=dev), torch.arange(L - 128, L, device=dev)])
+            res = {}
+            for order in ("sorted", "unsorted"):
+                rows = []
+                for _ in range(copies):
+                    pick = torch.rand(BG, L - 132, device=dev, generator=gen).topk(k, dim=1).indices + 4
+                    r = torch.cat([base.expand(BG, 132), pick], dim=1)
+                    r = r.sort(dim=1).values if order == "sorted" else r[:, torch.randperm(S, device=dev)]
+                    rows.append(r.to(torch.int32).contiguous())
+
+                def att(i):
+                    nat.call("attnlab_attend", K[i].data_ptr(), V[i].data_ptr(), L * d, d, q.data_ptr(),
+                             rows[i].data_ptr(), S, B, G, h, S, L, P, 1.0 / math.sqrt(d), out.data_ptr(), 1,
+                             part.data_ptr(), stream())
+                res[order] = time_rotating(torch, att, copies)
+            ab = BG * (S * d * 2 * 2 + 4 * S + 2 * h * d * 2)
+            emit({"sweep": "attend", "batch": B, "L": L, "k": k, "rows": S, "partitions": P,
+                  "sorted_us": res["sorted"], "unsorted_us": res["unsorted"],
+                  "sorted_gbs": ab / res["sorted"] / 1e3, "dense_us": us_dense,
+                  "speedup_vs_dense": us_dense / max(res["sorted"], res["unsorted"])})
+        del K, V
+        torch.cuda.empty_cache()
+
+
+def run_sweeps(torch, dev, which="all"):
+    def emit(d):
+        print(json.dumps(d), flush=True)
+    if which in ("all", "attend"):
+        sweep_attend(torch, dev, emit)
+    if which in ("all", "score"):
+        sweep_lightning_topk(torch, dev, emit)
+    return 0
+
+
+# ---------------------------------------------------------------------------------------------------------------------
 # CPU baseline: the reference's op sequence on the host cores
 # ---------------------------------------------------------------------------------------------------------------------
 def cpu_baseline(torch, ls, budget_s, layers_in_step):
@@ -512,6 +665,8 @@ def main() -> int:
         return pmc_workload(torch, dev, args)
     if args.prefill_workload:
         return prefill_workload(torch, dev)
+    if args.sweeps:
+        return run_sweeps(torch, dev, args.sweeps)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,

@@ -131,6 +131,17 @@ int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k,
                  float* top_val, int64_t top_stride, void* stream);
 
 /*
+ * attnlab_topk spread over the chip for long rows (the same selection, bit for bit): a histogram pass, a classify
+ * pass over tiles of 4096 scores and one resolve workgroup per row, instead of one workgroup per row for every pass.
+ * Replaces the same torch.topk call (decode.py:86-93). state: [R, ATTNLAB_SELECT_STATE_WORDS] uint32, 16-byte
+ * aligned, zero on entry and left zero; scratch: at least attnlab_select_scratch_bytes(R, M) bytes, no
+ * initialisation. Rows longer than 262144 scores run the single-workgroup select. Score order needs k <= 4096.
+ */
+int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, int k, int order, int32_t* top_idx,
+                       float* top_val, int64_t top_stride, uint32_t* state, void* scratch, int64_t scratch_bytes,
+                       void* stream);
+
+/*
  * Selection of one decode step: top-k over the candidate scores merged with the fixed set F, written as the row
  * list the attend kernel reads. Replaces select_rows_kernel + the optional canonical sort
  * (decode.py:86-93, :160-161) and DecodeRequest.select_positions (decode.py:50-56).

@@ -28,16 +28,18 @@ def heavy_tail(R, M, seed, frac=0.02, sigma=3.0):
 
 
 def check_topk(gpu, s: np.ndarray, k: int):
+    """Both selections (one workgroup per row; histogram + classify + resolve over the chip) against the oracle."""
     t = torch.from_numpy(s).to(gpu)
     for order in ("score", "position"):
         if order == "score" and k > hip_select.MAX_SCORE_ORDER_K:
             continue
-        vals, idx = hip_select.topk(t, k, order=order)
-        torch.cuda.synchronize()
         want = exact.topk(s, k, order=order)
-        got = idx.cpu().numpy()
-        assert np.array_equal(got, want), f"order={order} M={s.shape[-1]} k={k}: indices differ"
-        np.testing.assert_array_equal(vals.cpu().numpy(), np.take_along_axis(s, want, -1))
+        for tiled in (False, True):
+            vals, idx = hip_select.topk(t, k, order=order, tiled=tiled)
+            torch.cuda.synchronize()
+            got = idx.cpu().numpy()
+            assert np.array_equal(got, want), f"order={order} M={s.shape[-1]} k={k} tiled={tiled}: indices differ"
+            np.testing.assert_array_equal(vals.cpu().numpy(), np.take_along_axis(s, want, -1))
 
 
 @pytest.mark.parametrize("M", [1, 5, 100, 1000, 4093, 32700, 32768, 40000, 65468, 131008])
@@ -82,9 +84,10 @@ def test_nan_signed_zero_and_infinities(gpu):
             if k > 4096:
                 continue
             t = torch.from_numpy(s).to(gpu)
-            _, idx = hip_select.topk(t, k, order=order)
-            torch.cuda.synchronize()
-            assert np.array_equal(idx.cpu().numpy(), exact.topk(s, k, order=order)), (k, order)
+            for tiled in (False, True):
+                _, idx = hip_select.topk(t, k, order=order, tiled=tiled)
+                torch.cuda.synchronize()
+                assert np.array_equal(idx.cpu().numpy(), exact.topk(s, k, order=order)), (k, order, tiled)
 
 
 @pytest.mark.parametrize("legal,k0,order", [(2048, 64, "position"), (2048, 64, "score"), (300, 37, "score"),
@@ -204,7 +207,7 @@ def specials(rng, shape):
                                      (32704, 32704, "normal"), (5000, 4999, "ties")])
 def test_tiled_select_matches_the_oracle(gpu, M, k, gen):
     """Tiled select (4096-key tiles classified, one workgroup per row resolves) vs the oracle: plain, ties at the
-    threshold (taken in index order), more than 4096 candidates sharing the threshold's first digit (streaming
+    threshold (taken in index order), more than 8192 candidates sharing the threshold's first digit (streaming
     fallback), NaN / +-0 / +-inf, k = M, long rows, a row too long for the tiled path (262144 < M); the state is left
     zeroed and a second call on other data is exact too."""
     rng = np.random.default_rng(M + k)
