@@ -409,16 +409,18 @@ static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
 //                      gathers the candidates' scores, finds the threshold among them with the remaining two radix
 //                      digits, takes the tied keys at the threshold in index order, ORs the selected candidates into
 //                      the "above" bitmap in LDS and writes the set bits in index order (plus F), or in score order
-//                      after one LDS sort; it then clears the row's histogram. A row with more than kCandCap candidates
+//                      after one LDS sort; it then clears the row's histogram. A row with more than CAP candidates
 //                      runs the single-workgroup select.
 // Every kernel issues its global loads before it uses any of them: each is a few memory round trips long.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int kTileKeys = 4096;
 constexpr int kTileThreads = 256;
 constexpr int kTileKPT = kTileKeys / kTileThreads;   // 16 keys per thread, one contiguous segment (half a bitmap word)
-constexpr int kCandCap = 8192;                        // candidates per row, listed in LDS (in sortbuf)
-constexpr int kCandPerThread = kCandCap / kSelThreads;
-static_assert(kCandCap * sizeof(uint32_t) <= sizeof(SelectShared::sortbuf), "the candidate list lives in sortbuf");
+// Candidates per row listed in LDS (in sortbuf): 4096 while rows are at most 64K long (a first-digit bin there holds a
+// few thousand keys at most for any smooth distribution), 8192 beyond, where the larger list costs ~2 us of resolve
+constexpr int kCandCapShort = 4096, kCandCapLong = 8192;
+constexpr int kCandCapLongFromM = 65537;
+static_assert(kCandCapLong * sizeof(uint32_t) <= sizeof(SelectShared::sortbuf), "the candidate list lives in sortbuf");
 constexpr int kMaxWords = 8192;                       // bitmap words per row held in LDS: M <= 262144
 constexpr int kMaxWordsPerThread = kMaxWords / kSelThreads;
 
@@ -518,7 +520,9 @@ __global__ __launch_bounds__(kTileThreads) void select_hist(SelectArgs a, TiledA
     flush_histogram<kTileThreads>(hsh, a.hist, row);
 }
 
+template <int CAP>
 __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, TiledArgs t) {
+    constexpr int kCandPerThread = CAP / kSelThreads;
     __shared__ SelectShared sh;                 // sortbuf holds the candidate list (as uint32 indices)
     __shared__ __attribute__((aligned(16))) uint32_t hist3[1024];
     __shared__ uint32_t bits[kMaxWords];
@@ -550,7 +554,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     }
     uint32_t ec, unused, n, n_above;
     block_scan2<kSelThreads>(nc, na, ec, unused, n, n_above, sh.wave_tot);
-    if (n > (uint32_t)kCandCap) {   // too many keys share the threshold's first digit: single-workgroup select
+    if (n > (uint32_t)CAP) {   // too many keys share the threshold's first digit: single-workgroup select
         select_row_streaming(a, row, sh);
         return;
     }
@@ -563,7 +567,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
         while (word) {
             const uint32_t b = __ffs(word) - 1;
             word &= word - 1;
-            if (pos < (uint32_t)kCandCap) list[pos] = (uint32_t)(w0 + j) * 32u + b;
+            if (pos < (uint32_t)CAP) list[pos] = (uint32_t)(w0 + j) * 32u + b;
             ++pos;
         }
     }
@@ -629,6 +633,36 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     }
     uint32_t slot, unused3, tsel, unused_t3;
     block_scan2<kSelThreads>(ns, 0u, slot, unused3, tsel, unused_t3, sh.wave_tot);
+    uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
+    if (a.order == ATTNLAB_ORDER_POSITION && !a.top_idx && !a.top_val) {
+        // the decode step's row list: candidates at slots lo.., then F, written directly
+        const int nrec = a.legal - a.hi, S = a.lo + nrec + a.k, nf = a.lo + nrec;
+        int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride : nullptr;
+        int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S : nullptr;
+        const int64_t base = (int64_t)row * a.C;
+#pragma unroll
+        for (int j = 0; j < kMaxWordsPerThread; ++j) {
+            uint32_t word = sw[j];
+            while (word) {
+                const uint32_t b = __ffs(word) - 1;
+                word &= word - 1;
+                const int idx = (w0 + j) * 32 + (int)b;
+                if (slot < (uint32_t)a.k) {
+                    if (rows) rows[a.lo + slot] = a.lo + idx;
+                    if (flat) flat[a.lo + slot] = base + a.lo + idx;
+                }
+                ++slot;
+            }
+        }
+        for (int f = tid; f < nf; f += kSelThreads) {
+            const int p = f < a.lo ? f : a.hi + (f - a.lo);
+            const int s_out = f < a.lo ? f : a.lo + a.k + (f - a.lo);
+            if (rows) rows[s_out] = p;
+            if (flat) flat[s_out] = base + p;
+        }
+        for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
+        return;
+    }
     const Emitter em = make_emitter(a, row, sh);
     const bool by_score = a.order == ATTNLAB_ORDER_SCORE;
 #pragma unroll
@@ -641,7 +675,6 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
             em.put(slot++, idx, by_score ? score_key(srow[idx]) : 0u);
         }
     }
-    uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
     for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
@@ -650,7 +683,8 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
 static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s, bool build_hist = false) {
     if (build_hist) hipLaunchKernelGGL(select_hist, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
     hipLaunchKernelGGL(select_classify, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
-    hipLaunchKernelGGL(select_resolve, dim3(R), dim3(kSelThreads), 0, s, a, t);
+    if (a.M >= kCandCapLongFromM) hipLaunchKernelGGL(select_resolve<kCandCapLong>, dim3(R), dim3(kSelThreads), 0, s, a, t);
+    else hipLaunchKernelGGL(select_resolve<kCandCapShort>, dim3(R), dim3(kSelThreads), 0, s, a, t);
     return check_launch("select_tiled");
 }
 
