@@ -11,7 +11,7 @@ import torch
 
 from . import _native as nat
 
-MAX_SCORE_ORDER_K = 4096
+MAX_SCORE_ORDER_K = 8192
 TILED_MIN_M = 32768     # rows at least this long are selected by the tiled kernels (attnlab_topk_tiled)
 TILED_MAX_M = 262144    # ... and at most this long (longer rows take the single-workgroup select)
 ORDERS = {"position": nat.ORDER_POSITION, "score": nat.ORDER_SCORE}

@@ -21,7 +21,7 @@ namespace attnlab {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kMaxScoreOrderK = 4096;
+constexpr int kMaxScoreOrderK = 8192;   // score order sorts the k selected pairs in LDS (64 KB)
 
 struct SelectArgs {
     const float* scores;

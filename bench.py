@@ -67,6 +67,12 @@ def parse_args():
     ap.add_argument("--sweeps", nargs="?", const="all", choices=("all", "score", "attend"),
                     help="instead of the bench line: the microbenchmark sweeps of BASELINE configs[1] (lightning score "
                          "+ top-k) and configs[2] (gather-free attend vs dense), one JSON line per case")
+    ap.add_argument("--c4", action="store_true",
+                    help="instead of the bench line: BASELINE configs[3], a random-init Qwen3-1.7B-shaped model read "
+                         "through the wrapper: 8192-token prompt, 128 greedy steps on the full read, the same tokens on "
+                         "the sparse read (rho = 1/32); per-step logits compared, one JSON line")
+    ap.add_argument("--c4-steps", type=int, default=128)
+    ap.add_argument("--c4-prompt", type=int, default=8192)
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
@@ -555,6 +561,111 @@ def sweep_attend(torch, dev, emit):
         torch.cuda.empty_cache()
 
 
+def qwen3_1p7b(torch, dev, seed):
+    """BASELINE configs[3]'s model shape with random bf16 weights ~ N(0, 0.02) (transformers' own init), on `dev`."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=40960,
+                      rope_theta=1_000_000.0, rms_norm_eps=1e-6, tie_word_embeddings=True, initializer_range=0.02,
+                      attn_implementation="sdpa")
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = Qwen3ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    for p in model.parameters():
+        p.requires_grad_(False)
+    return model
+
+
+def run_c4(torch, dev, args):
+    """configs[3] through the wrapper on the HIP kernels: greedy decode on the full read (A); the same tokens on the
+    sparse read (D0, rho = 1/32) and on the sparse read with k0 = capacity (every candidate selected, which must
+    equal A); the full read against the unwrapped model in float32 with transformers' eager attention."""
+    from attention_lab.qwen_wrap import LabRunner, make_state, unwrap_model, wrap_model
+    T0, steps = args.c4_prompt, args.c4_steps
+    t_setup = time.perf_counter()
+    model = qwen3_1p7b(torch, dev, args.seed)
+    holder = wrap_model(model)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    prompt = torch.randint(0, model.config.vocab_size, (1, T0), device=dev, generator=gen)
+    cap = T0 + steps + 1
+    print(f"[c4] model ready in {time.perf_counter() - t_setup:.1f}s", file=sys.stderr, flush=True)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        out = fn()
+        torch.cuda.synchronize()
+        return out, time.perf_counter() - t
+
+    def compare(a, b):
+        """a, b: [steps, V] float32 logits."""
+        lp, lq = torch.log_softmax(b, -1), torch.log_softmax(a, -1)
+        return {"top1_agreement": float((a.argmax(-1) == b.argmax(-1)).float().mean()),
+                "max_abs_diff": float((a - b).abs().max()),
+                "rel_norm_diff": float((a - b).norm() / b.norm()),
+                "kl_mean": float((lp.exp() * (lp - lq)).sum(-1).mean())}
+
+    res = {}
+    with torch.inference_mode():
+        full = LabRunner(model, holder, make_state(model, cap, "full"))
+        logits, res["prefill_s_full"] = timed(lambda: full.prefill(prompt, 1024))
+        tokens, full_logits = [], []
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+
+        def decode_full():
+            nonlocal tok
+            for _ in range(steps):
+                tokens.append(tok)
+                lg = full.step(tok)[:, -1].float()
+                full_logits.append(lg)
+                tok = lg.argmax(-1, keepdim=True)
+        _, t = timed(decode_full)
+        res["decode_ms_full"] = t * 1e3 / steps
+        full_logits = torch.cat(full_logits)
+        del full
+        print(f"[c4] full read done ({res['prefill_s_full']:.1f}s prefill)", file=sys.stderr, flush=True)
+
+        def sparse_run(k0):
+            # k0 = capacity selects up to 8252 candidates: position order (canonical_order) keeps any k
+            st = make_state(model, cap, "sparse", selector="index", r=32, seed=args.seed, canonical_order=k0 is not None)
+            runner = LabRunner(model, holder, st)
+            _, t_pf = timed(lambda: runner.prefill(prompt, 1024))
+            k = st.begin_request(args.rho, k0=k0)
+            outs = []
+            _, t_dec = timed(lambda: [outs.append(runner.step(tokens[i])[:, -1].float()) for i in range(steps)])
+            return torch.cat(outs), t_pf, t_dec * 1e3 / steps, k
+
+        sp, res["prefill_s_sparse"], res["decode_ms_sparse"], k0 = sparse_run(None)
+        res["sparse_vs_full"] = compare(sp, full_logits)
+        allk, _, _, kcap = sparse_run(cap)
+        res["sparse_k0_capacity_vs_full"] = compare(allk, full_logits)
+        print(f"[c4] sparse reads done (k0 = {k0}, then {kcap})", file=sys.stderr, flush=True)
+        del sp, allk
+        # reference: the unwrapped model in float32, eager attention, one forward over prompt + generated tokens
+        unwrap_model(model)
+        ref_model = model.float()
+        ref_model.config._attn_implementation = "eager"
+        ids = torch.cat([prompt] + tokens, dim=1)
+        # logits of positions T0 - 1 .. T0 + steps - 1; step i fed token i at position T0 + i
+        ref = ref_model(input_ids=ids, use_cache=False, logits_to_keep=steps + 1).logits[0, 1:].float()
+        res["full_vs_float32_eager_reference"] = compare(full_logits, ref)
+    print(json.dumps({
+        "workload": f"configs[3]: random-init Qwen3-1.7B shape (28 layers, hidden 2048, 16q/8kv, d=128, FFN 6144, "
+                    f"vocab 151936, bf16 ~ N(0, 0.02)), {T0}-token uniform prompt, {steps} greedy steps on the full "
+                    f"read; the same tokens (teacher-forced) on the sparse read (rho={args.rho}, k0={k0}, one r=32 "
+                    f"grouped indexer per layer) and on the sparse read with k0 = capacity; whole model on the GPU, "
+                    f"attention through the HIP kernels",
+        **res,
+        "note": "the indexers are untrained (random), so the rows they pick are unrelated to the attention scores, and "
+                "random weights spread the attention mass over the whole context: a 1/32 read then does not reproduce "
+                "the full read's logits (sparse_vs_full measures that). k0 = capacity selects every candidate and must "
+                "reproduce the full read up to bf16 rounding and summation order",
+    }))
+    return 0
+
+
 def run_sweeps(torch, dev, which="all"):
     def emit(d):
         print(json.dumps(d), flush=True)
@@ -667,6 +778,8 @@ def main() -> int:
         return prefill_workload(torch, dev)
     if args.sweeps:
         return run_sweeps(torch, dev, args.sweeps)
+    if args.c4:
+        return run_c4(torch, dev, args)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,

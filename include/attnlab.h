@@ -135,7 +135,7 @@ int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k,
  * pass over tiles of 4096 scores and one resolve workgroup per row, instead of one workgroup per row for every pass.
  * Replaces the same torch.topk call (decode.py:86-93). state: [R, ATTNLAB_SELECT_STATE_WORDS] uint32, 16-byte
  * aligned, zero on entry and left zero; scratch: at least attnlab_select_scratch_bytes(R, M) bytes, no
- * initialisation. Rows longer than 262144 scores run the single-workgroup select. Score order needs k <= 4096.
+ * initialisation. Rows longer than 262144 scores run the single-workgroup select. Score order needs k <= 8192.
  */
 int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, int k, int order, int32_t* top_idx,
                        float* top_val, int64_t top_stride, uint32_t* state, void* scratch, int64_t scratch_bytes,
@@ -148,7 +148,7 @@ int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, 
  * scores: [B*G] rows of M = hi - lo candidate scores (row stride score_stride). F = [0, lo) U [hi, legal).
  * S = lo + (legal - hi) + k. rows: [B*G, S] int32 positions (row stride rows_stride; nullable). rows_flat: [B*G*S]
  * int64 flat row ids pos + (b*G+g)*C of the flattened [B*G*C, d] cache (sparse.py:14-16; nullable).
- * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE (the latter needs k <= 4096).
+ * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE (the latter needs k <= 8192).
  * state (nullable): the select state [B*G, ATTNLAB_SELECT_STATE_WORDS] attnlab_score_grouped filled for these scores;
  * when given, the first radix pass is skipped and the state is left zeroed for the next call.
  * scratch (nullable, 4-byte aligned, no zeroing needed): with state, position order, 0 < k, hi - lo <= 262144 and

@@ -59,6 +59,12 @@ def test_topk_position_order_large_k(gpu, M, k):
     assert np.array_equal(idx.cpu().numpy(), exact.topk(s, k, order="position"))
 
 
+@pytest.mark.parametrize("M,k", [(20000, 6000), (70000, 8192)])
+def test_score_order_beyond_4096(gpu, M, k):
+    """Score order sorts up to 8192 selected pairs in LDS (both selections)."""
+    check_topk(gpu, heavy_tail(2, M, seed=k), k)
+
+
 def test_ties_resolve_to_the_lowest_index(gpu):
     rng = np.random.default_rng(7)
     for M, levels in ((1000, 3), (5000, 17), (32700, 50)):
@@ -244,7 +250,7 @@ def test_validation(gpu):
     with pytest.raises(ValueError):
         hip_select.topk(t.double(), 3)
     with pytest.raises(ValueError):
-        hip_select.topk(torch.zeros(2, 10000, device=gpu), 5000, order="score")
+        hip_select.topk(torch.zeros(2, 10000, device=gpu), 9000, order="score")
     with pytest.raises(ValueError):
         hip_select.topk(t, 3, order="random")
     with pytest.raises(ValueError):
