@@ -4,9 +4,9 @@ Same signature and validation as the reference's full_attention (src/attention_l
 name of the reference is accepted; all of them read K and V once per KV group (the reference's sdpa_fold
 behaviour), which is the only layout the HIP kernel has. A single query at the last legal position needs no mask
 (full.py:29). Several queries (a prefill chunk) follow the reference's legality rule (reference.py:41-48: key j is
-legal for query t iff j <= its position and j < valid_length): query t is one dense-decode launch over the first
-min(position_t + 1, valid_length) positions. That is exact and stays on the HIP kernel, at one launch per query
-position; a prefill GEMM kernel is not part of this build.
+legal for query t iff j <= its position and j < valid_length). Consecutive positions (a prefill chunk) run the causal
+prefill kernel on the matrix cores in one launch; any other position list runs one dense-decode launch per query
+over the first min(position_t + 1, valid_length) positions.
 """
 from __future__ import annotations
 
@@ -45,6 +45,10 @@ def full_attention(q, k, v, *, valid_length=None, query_positions=None, scale=No
     if T == 1 and qp[0] >= legal - 1:
         out = hip_attend.dense_decode(q.reshape(B, G, h, d).contiguous(), k, v, legal, scale=scale, out_dtype=q.dtype)
         return out.view(B, G, h, 1, d)
+    if (q.dtype == torch.bfloat16 and h in hip_attend.PREFILL_HEADS and d == hip_attend.HEAD_DIM
+            and qp == list(range(qp[0], qp[0] + T))):
+        # consecutive positions (a prefill chunk): one launch of the causal prefill kernel
+        return hip_attend.prefill_attend(q.contiguous(), k, v, qp[0], legal, scale=scale)
     out = torch.empty(B, G, h, T, d, dtype=q.dtype, device=q.device)
     for t, p in enumerate(qp):
         out[:, :, :, t] = hip_attend.dense_decode(q[:, :, :, t].contiguous(), k, v, min(p + 1, legal), scale=scale,

@@ -217,3 +217,35 @@ def dense_decode(q, k, v, valid_length: int, *, scale=None, partitions=None, out
     nat.call("attnlab_dense_decode", k.data_ptr(), v.data_ptr(), C * HEAD_DIM, HEAD_DIM, q.data_ptr(), B, G, h, L, C,
              P, sc, out.data_ptr(), int(out.dtype == torch.bfloat16), nat.ptr(part), nat.stream_of(k.device))
     return out
+
+
+PREFILL_HEADS = (1, 2, 4, 8, 16)
+
+
+def prefill_attend(q, k, v, q_pos0: int, valid_length: int, *, scale=None, out=None):
+    """Causal prefill read on the matrix cores: q [B,G,h,T,d] at positions q_pos0 .. q_pos0 + T - 1, k/v [B,G,C,d];
+    query t reads the cache rows j <= q_pos0 + t, j < valid_length. Returns bf16 [B,G,h,T,d]."""
+    if k.dim() != 4 or k.dtype != torch.bfloat16 or not k.is_contiguous() or not k.is_cuda:
+        raise ValueError("the cache must be a contiguous bfloat16 [B, G, C, d] tensor on a HIP device")
+    if v.shape != k.shape or v.dtype != k.dtype or not v.is_contiguous() or v.device != k.device:
+        raise ValueError("v must match k")
+    B, G, C, d = k.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"head_dim must be {HEAD_DIM}")
+    if q.dim() != 5 or tuple(q.shape[:2]) != (B, G) or q.shape[4] != d or q.dtype != torch.bfloat16 \
+            or not q.is_contiguous() or q.device != k.device:
+        raise ValueError("q must be a contiguous bfloat16 [B, G, h, T, d] tensor on the cache device")
+    h, T = int(q.shape[2]), int(q.shape[3])
+    if h not in PREFILL_HEADS:
+        raise ValueError(f"h={h} must be one of {PREFILL_HEADS}")
+    L, p0 = int(valid_length), int(q_pos0)
+    if not 0 < L <= C or p0 < 0:
+        raise ValueError(f"need 0 < valid_length <= capacity and q_pos0 >= 0 (got {L}, {C}, {p0})")
+    if out is None:
+        out = torch.empty(B, G, h, T, d, dtype=torch.bfloat16, device=k.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(q.shape) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 tensor shaped like q")
+    sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    nat.call("attnlab_prefill_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), C * d, d, out.data_ptr(), B, G, h, T,
+             d, p0, L, C, sc, nat.stream_of(k.device))
+    return out

@@ -354,6 +354,209 @@ __global__ __launch_bounds__(256) void project_keys_mfma(ProjectArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// Causal prefill attention on the matrix cores: T queries at consecutive positions q_pos0 + t of one KV group,
+// every query head of the group, against the cache rows j <= q_pos0 + t, j < legal (the legality rule of
+// reference.py:41-48, the full read of full.py:17-44 for a prefill chunk):
+//   out[bg, i, t, :] = sum_j softmax_j(scale * q[bg, i, t] . K[bg, j]) V[bg, j]
+// A workgroup owns 128 (query, head) rows: 128 / h consecutive positions with all h heads of the group, so each K/V
+// block is read once for every head. Per block of 64 keys:
+//   S^T = K Q^T    v_mfma_f32_32x32x16_bf16, A = 32 keys x 16 dims (LDS, row-major), B = Q^T (registers); lane l's
+//                  column is its own query row, so the softmax state of a row lives in lanes n and n + 32
+//   P^T           online softmax in the log2 domain on the accumulators; the C layout of S^T is already the B
+//                  layout P^T needs for the next product (keys 8 (i/4) + 4 (l/32) + i%4 of row l%32)
+//   O^T += V^T P^T A = 32 dims x 16 keys from V^T in LDS (staged transposed, two keys per 32-bit word), B = P^T
+// O^T keeps each row's 128 outputs in the lanes of that row, so rescaling needs no exchange. The next block's K/V
+// is loaded into registers while the current one is computed.
+// ---------------------------------------------------------------------------------------------------------------
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
+
+struct PrefillAttendArgs {
+    const uint16_t* q;      // [BG, h, T, 128]
+    const uint16_t* K;      // row j of bg at K + bg * kv_bg_stride + j * kv_row_stride
+    const uint16_t* V;
+    int64_t kv_bg_stride;
+    int kv_row_stride;
+    uint16_t* out;          // [BG, h, T, 128]
+    int h, T, q_pos0, legal;
+    int qtiles;             // ceil(T / (128 / h))
+    float scale_log2;
+};
+
+constexpr int kPaRows = 128;          // (query, head) rows per workgroup: 4 waves x 32
+constexpr int kPaKeys = 64;           // keys per block
+constexpr int kPaKPitch = 128 + 8;    // bf16 per K row in LDS (272 bytes: 16-byte aligned rows)
+constexpr int kPaVPitch = 64 + 4;     // bf16 per V^T row in LDS (136 bytes)
+constexpr float kPaLazy = 8.0f;       // rescale O only when the running max grows by more than 2^8
+
+// two fp32 -> packed bf16 pair, round to nearest even (gfx950 converts in hardware: v_cvt_pk_bf16_f32)
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+    const bf16x2v_t v = {(__bf16)x, (__bf16)y};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__global__ __launch_bounds__(256) void prefill_attend(PrefillAttendArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kPaKeys * kPaKPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[128 * kPaVPitch];
+    const int lin = xcd_contiguous_block();
+    const int bg = lin / a.qtiles, qt = lin - bg * a.qtiles;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int BQ = kPaRows / a.h;
+    const int t0 = qt * BQ;
+    const int R = 32 * wave + n;                 // this lane's row: query t0 + R / h, head R % h
+    const int t = t0 + R / a.h, head = R % a.h;
+    const int tc = min(t, a.T - 1);
+    const int pos = a.q_pos0 + tc;
+    bf16x8_t qb[8];                              // B operand of S^T: row R, dims 16 kk + 8 g .. + 7
+    {
+        const uint16_t* qr = a.q + (((size_t)bg * a.h + head) * a.T + tc) * 128 + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qr + 16 * kk));
+    }
+    const int kend = min(a.legal, a.q_pos0 + min(t0 + BQ, a.T));                          // keys of the workgroup
+    const int wave_first = a.q_pos0 + min(t0 + (32 * wave) / a.h, a.T - 1);
+    const int kend_wave = min(a.legal, a.q_pos0 + min(t0 + (32 * wave + 31) / a.h, a.T - 1) + 1);
+
+    const uint16_t* Kb = a.K + (size_t)bg * a.kv_bg_stride;
+    const uint16_t* Vb = a.V + (size_t)bg * a.kv_bg_stride;
+    // staging: K chunk c = tid + 256 u -> key c / 16, 16 bytes at dim 8 (c % 16); V unit w = tid + 256 u -> dims
+    // 8 (w % 16) .. + 7 of keys 2 (w / 16) and 2 (w / 16) + 1 (16 lanes read one key's 256 bytes)
+    u32x4_t kr[4], vr[2][2];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = tid + 256 * u;
+            const int key = min(kb + (c >> 4), kend - 1);
+            kr[u] = *reinterpret_cast<const u32x4_t*>(Kb + (size_t)key * a.kv_row_stride + 8 * (c & 15));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int w = tid + 256 * u;
+            const int k0 = min(kb + 2 * (w >> 4), kend - 1), k1 = min(kb + 2 * (w >> 4) + 1, kend - 1);
+            vr[u][0] = *reinterpret_cast<const u32x4_t*>(Vb + (size_t)k0 * a.kv_row_stride + 8 * (w & 15));
+            vr[u][1] = *reinterpret_cast<const u32x4_t*>(Vb + (size_t)k1 * a.kv_row_stride + 8 * (w & 15));
+        }
+    };
+    auto lds_store = [&]() {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = tid + 256 * u;
+            *reinterpret_cast<u32x4_t*>(&ks[(c >> 4) * kPaKPitch + 8 * (c & 15)]) = kr[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int w = tid + 256 * u;
+            const int kp = w >> 4, d0 = 8 * (w & 15);
+            const uint32_t x[4] = {vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w};
+            const uint32_t y[4] = {vr[u][1].x, vr[u][1].y, vr[u][1].z, vr[u][1].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {   // dims d0 + 2e, d0 + 2e + 1: (key 2kp, key 2kp + 1) pairs
+                *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * e) * kPaVPitch + 2 * kp]) = (x[e] & 0xffffu) | (y[e] << 16);
+                *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * e + 1) * kPaVPitch + 2 * kp]) = (x[e] >> 16) | (y[e] & 0xffff0000u);
+            }
+        }
+    };
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x16_t o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
+
+    gload(0);
+    for (int kb = 0; kb < kend; kb += kPaKeys) {
+        if (kb) __syncthreads();   // the previous block's LDS reads are done
+        lds_store();
+        __syncthreads();
+        if (kb + kPaKeys < kend) gload(kb + kPaKeys);
+        if (kb >= kend_wave) continue;   // every row of this wave ends before the block (no barrier skipped: the
+                                         // loop's barriers are at its top)
+        f32x16_t s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kt][i] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const bf16x8_t ka = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const u32x4_t*>(&ks[(32 * kt + n) * kPaKPitch + 16 * kk + 8 * g]));
+                s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[kk], s[kt], 0, 0, 0);
+            }
+        }
+        // this lane's scores: row R, keys kb + 32 kt + 8 (i / 4) + 4 g + i % 4
+        const bool full = kb + kPaKeys - 1 <= wave_first && kb + kPaKeys <= a.legal;   // no key of the block masked
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float v = s[kt][i] * a.scale_log2;
+                if (!full) {
+                    const int key = kb + 32 * kt + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key > pos || key >= a.legal) v = -INFINITY;
+                }
+                s[kt][i] = v;
+                bm = fmaxf(bm, v);
+            }
+        bm = fmaxf(bm, shfl_xor_f32(bm, 32));
+        if (bm > m_run + kPaLazy) {   // also the first block of the row (m_run = -inf)
+            const float al = fast_exp2(m_run - bm);   // exp2(-inf) = 0
+            l_run *= al;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= al;
+            m_run = bm;
+        }
+        // P^T (bf16) as the B operand of O^T += V^T P^T, one per 16-key step ks: tile ks / 2, accumulators
+        // 8 (ks % 2) .. + 7, i.e. keys 16 (ks % 2) + 4 g + {0..3, 8..11} of the tile
+        bf16x8_t pb[4];
+#pragma unroll
+        for (int ks2 = 0; ks2 < 4; ++ks2) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p0 = m_run == -INFINITY ? 0.0f : fast_exp2(s[ks2 >> 1][8 * (ks2 & 1) + 2 * e] - m_run);
+                const float p1 = m_run == -INFINITY ? 0.0f : fast_exp2(s[ks2 >> 1][8 * (ks2 & 1) + 2 * e + 1] - m_run);
+                l_run += p0 + p1;
+                w4[e] = pack_bf16x2(p0, p1);
+            }
+            pb[ks2] = __builtin_bit_cast(bf16x8_t, u32x4_t{w4[0], w4[1], w4[2], w4[3]});
+        }
+#pragma unroll
+        for (int ks2 = 0; ks2 < 4; ++ks2) {
+            const int key0 = 32 * (ks2 >> 1) + 16 * (ks2 & 1) + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint16_t* vrow = &vt[(32 * dt + n) * kPaVPitch + key0];
+                const u32x2v_t lo4 = *reinterpret_cast<const u32x2v_t*>(vrow);
+                const u32x2v_t hi4 = *reinterpret_cast<const u32x2v_t*>(vrow + 8);
+                const bf16x8_t va = __builtin_bit_cast(bf16x8_t, u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y});
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[ks2], o[dt], 0, 0, 0);
+            }
+        }
+    }
+    const float l_tot = l_run + shfl_xor_f32(l_run, 32);
+    if (t >= a.T) return;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t* orow = a.out + (((size_t)bg * a.h + head) * a.T + t) * 128;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {   // dims 32 dt + 8 i4 + 4 g + 0..3
+            const f32x16_t& od = o[dt];
+            *reinterpret_cast<u32x2v_t*>(orow + 32 * dt + 8 * i4 + 4 * g) =
+                u32x2v_t{pack_bf16x2(od[4 * i4] * inv, od[4 * i4 + 1] * inv),
+                         pack_bf16x2(od[4 * i4 + 2] * inv, od[4 * i4 + 3] * inv)};
+        }
+}
+
 }  // namespace
 }  // namespace attnlab
 
@@ -424,4 +627,28 @@ extern "C" int attnlab_score_lightning_batched(const uint16_t* keys, int key_dty
     else LAUNCH_LB(8);
 #undef LAUNCH_LB
     return check_launch("lightning_batched");
+}
+
+extern "C" int attnlab_prefill_attend(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride,
+                                      int kv_row_stride, uint16_t* out, int B, int G, int h, int T, int d,
+                                      int q_pos0, int legal, int C, float scale, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && T >= 0, "B, G must be positive and T >= 0 (B=%d G=%d T=%d)", B, G, T);
+    ATTNLAB_REQUIRE(d == 128, "head_dim must be 128, got %d", d);
+    ATTNLAB_REQUIRE(h == 1 || h == 2 || h == 4 || h == 8 || h == 16, "query heads per group h=%d must divide 128 "
+                    "(1, 2, 4, 8 or 16)", h);
+    ATTNLAB_REQUIRE(q_pos0 >= 0 && 0 < legal && legal <= C, "need q_pos0 >= 0 and 0 < legal <= C (q_pos0=%d "
+                    "legal=%d C=%d)", q_pos0, legal, C);
+    if (T == 0) return ATTNLAB_OK;
+    ATTNLAB_REQUIRE(q && K && V && out, "q, K, V and out are required");
+    ATTNLAB_REQUIRE(kv_row_stride >= 128 && kv_row_stride % 8 == 0 && kv_bg_stride % 8 == 0 &&
+                        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(K) |
+                          reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
+                    "q, K, V, out and the K/V rows must be 16-byte aligned");
+    PrefillAttendArgs a{q, K, V, kv_bg_stride, kv_row_stride, out, h, T, q_pos0, legal, 0, scale * kLog2e};
+    const int BQ = kPaRows / h;
+    a.qtiles = (T + BQ - 1) / BQ;
+    const int64_t blocks = (int64_t)B * G * a.qtiles;
+    ATTNLAB_REQUIRE(blocks < (int64_t)1 << 31, "grid of %lld workgroups is too large", (long long)blocks);
+    hipLaunchKernelGGL(prefill_attend, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    return check_launch("prefill_attend");
 }

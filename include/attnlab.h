@@ -188,6 +188,18 @@ int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_t kv_bg_str
                          int out_bf16, float* part, void* stream);
 
 /*
+ * Causal prefill read on the matrix cores: full_attention (full.py:17-44) for a chunk of T > 1 queries, with the
+ * reference's legality rule (reference.py:41-48). Query t sits at position q_pos0 + t and reads the cache rows
+ * j <= q_pos0 + t, j < legal:
+ *   out[b,g,i,t,:] = sum_j softmax_j(scale * q[b,g,i,t,:] . K[b,g,j,:]) V[b,g,j,:]
+ * q, out: [B,G,h,T,d] bf16 contiguous; K/V row j of (b,g) at K + (b*G+g)*kv_bg_stride + j*kv_row_stride (elements).
+ * d must be 128; h one of 1, 2, 4, 8, 16; 16-byte aligned pointers and rows; 0 < legal <= C.
+ */
+int attnlab_prefill_attend(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride,
+                           int kv_row_stride, uint16_t* out, int B, int G, int h, int T, int d, int q_pos0, int legal,
+                           int C, float scale, void* stream);
+
+/*
  * Workspace (bytes) of attnlab_sparse_decode_step for these sizes: candidate scores, row list, u, tiled-select
  * scratch and split-K partials, each 256-byte aligned. Its contents need no initialisation.
  */
