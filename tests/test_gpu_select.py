@@ -189,6 +189,32 @@ def test_score_kernel_hands_over_the_first_digit_histogram(gpu, B, C, lo, hi, fu
     assert torch.equal(state.cpu(), state_for(s.cpu().numpy()))
 
 
+@pytest.mark.parametrize("G,C,lo,hi,fused", [(3, 32256, 4, 32000, False), (5, 20000, 4, 19500, True),
+                                             (1, 9000, 0, 8999, False)])
+def test_histogram_is_exact_when_a_row_spans_the_xcds(gpu, G, C, lo, hi, fused):
+    """Grids that are not a multiple of 8 keep the hardware's round-robin order, so the workgroups of one row run on
+    different XCDs (each with its own L2) and their histogram atomics meet only in memory: the state must still be
+    exactly the histogram of the scores."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_score
+    from attention_lab.indexer import GroupedIndexer
+    B, r, h, d = 1, 32, 2, 128
+    gen = torch.Generator().manual_seed(G * 11 + C)
+    zT = torch.randn(B, G, r, C, generator=gen).to(torch.bfloat16).to(gpu)
+    state = torch.zeros(B, G, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    for rep in range(3):
+        state.zero_()
+        if fused:
+            idx = GroupedIndexer(G, h, d, r, device=gpu, dtype=torch.bfloat16, seed=rep)
+            q_cat = torch.randn(B, G, h * d, generator=gen).to(torch.bfloat16).to(gpu)
+            s = hip_score.score_grouped(zT, lo, hi, q_cat=q_cat, wq_t=idx.wq_t_scaled, state=state)
+        else:
+            u = torch.randn(B, G, r, generator=gen).to(gpu)
+            s = hip_score.score_grouped(zT, lo, hi, u=u, state=state)
+        torch.cuda.synchronize()
+        assert torch.equal(state.cpu(), state_for(s.cpu().numpy())), f"rep {rep}"
+
+
 def tie_heavy(rng, shape):
     return rng.integers(0, 6, size=shape).astype(np.float32) * 0.25
 
