@@ -1,0 +1,101 @@
+"""bench.py's host side (no GPU): the one-GPU contract, the algorithmic byte counts behind `roofline.achieved`, and
+the rocprofv3 counter summaries behind `roofline.traffic` and the matrix-core busy fraction."""
+from __future__ import annotations
+
+import csv
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 2
+    line = json.loads(res.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
+
+
+def layer_stack(B, G, h, L, rho_k):
+    """A LayerStack's shape attributes without its tensors (the byte counts are arithmetic on them)."""
+    ls = bench.LayerStack.__new__(bench.LayerStack)
+    ls.B, ls.G, ls.h, ls.d, ls.r, ls.L, ls.C = B, G, h, 128, 32, L, L
+    ls.lo, ls.hi = 4, L - 64
+    ls.M = ls.hi - ls.lo
+    ls.k = rho_k
+    ls.S = 68 + rho_k
+    return ls
+
+
+def test_algorithmic_bytes_follow_the_per_unit_formulas():
+    """32K, rho = 1/32 (k = 1024, S = 1092), B = 1, G = 8, h = 2: the per-(b, g) figures of the measurement plan
+    (zT columns + fp32 scores; scores + indices; K/V rows + row ids + q + bf16 out; the whole dense read)."""
+    ls = layer_stack(1, 8, 2, 32768, 1024)
+    M = 32700
+    assert ls.score_bytes() == 8 * (32 * M * 2 + 4 * M + 32 * 2 + (2 * 128 + 128) * 2) + 8 * (2 * 128 * 32 + 32 * 128) * 2
+    assert 8 * (32 * M * 2 + 4 * M) == 17_788_800        # the zT read + score write part: 17.79 MB
+    assert ls.select_bytes() == 8 * (4 * M + 4 * 1024)
+    assert ls.attend_bytes() == 8 * (1092 * 512 + 4 * 1092 + 2 * 128 * 2 * 2)
+    assert ls.dense_bytes() == 8 * (32768 * 512 + 2 * 128 * 2 * 2)
+    big = layer_stack(16, 8, 4, 32768, 1024)
+    assert big.score_bytes() + big.select_bytes() + big.attend_bytes() == 374_773_760   # per layer at the bench shape
+
+
+def test_prefill_score_counts():
+    ps = bench.PrefillScore.__new__(bench.PrefillScore)
+    ps.B, ps.KG, ps.T, ps.L, ps.nh, ps.r = 1, 8, 8192, 8192, 4, 32
+    assert ps.scores() == 8 * 8192 * 8193 // 2 == 268_468_224
+    assert ps.algorithmic_bytes() == 4 * ps.scores() + 8 * (8192 * 64 + 8192 * 4 * 128 + 8192 * 16)
+    assert ps.flops() == ps.scores() * 4 * (64 + 2)
+
+
+def write_counters(path, rows):
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+
+
+def test_traffic_summary_scales_each_counter_by_the_copy(tmp_path, capsys):
+    copy = "__amd_rocclr_copyBuffer"
+    scan = f"void attnlab::{bench.SCAN_KERNEL}<4>(attnlab::ScoreArgs)"
+    fetch, write = str(tmp_path / "f"), str(tmp_path / "w")
+    # FETCH_SIZE counts half of what moves (the copy reads 256 MiB = 262144 KiB and shows 131072); small set-up copies
+    # are ignored
+    write_counters(fetch, [{"Kernel_Name": scan, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1000.0}] * 5 +
+                   [{"Kernel_Name": copy, "Counter_Name": "FETCH_SIZE", "Counter_Value": 131072.0}] * 5 +
+                   [{"Kernel_Name": copy, "Counter_Name": "FETCH_SIZE", "Counter_Value": 4.0}])
+    write_counters(write, [{"Kernel_Name": scan, "Counter_Name": "WRITE_SIZE", "Counter_Value": 300.0}] * 5 +
+                   [{"Kernel_Name": copy, "Counter_Name": "WRITE_SIZE", "Counter_Value": 262144.0}] * 5)
+    assert bench.pmc_summary(fetch, write) == 0
+    out = json.loads(capsys.readouterr().out)
+    assert out["fetch_scale"] == pytest.approx(2.0) and out["write_scale"] == pytest.approx(1.0)
+    assert out["traffic_bytes_per_launch"] == pytest.approx(1000 * 1024 * 2 + 300 * 1024)
+
+
+def test_mfma_busy_fraction(tmp_path, capsys):
+    k = f"void attnlab::{bench.PREFILL_KERNEL}<true, 4, true>(Args)"
+    rows = []
+    for name, v in (("SQ_VALU_MFMA_BUSY_CYCLES", 1024 * 1000.0), ("GRBM_GUI_ACTIVE", 8 * 4000.0),
+                    ("SQ_INSTS_MFMA", 64000.0), ("SQ_INSTS_VALU", 640000.0)):
+        rows.append({"Kernel_Name": k, "Counter_Name": name, "Counter_Value": v})
+    write_counters(str(tmp_path), rows)
+    assert bench.prefill_pmc_summary(str(tmp_path)) == 0
+    out = json.loads(capsys.readouterr().out)
+    assert out["mfma_busy_frac"] == pytest.approx(0.25)          # 1000 busy of 4000 cycles per SIMD
+    assert out["mfma_cycles_per_instruction"] == pytest.approx(16.0)
+    assert out["valu_instructions_per_mfma"] == pytest.approx(10.0)
+
+
+def test_committed_profiles_feed_the_bench_line():
+    assert bench.measured_traffic() == pytest.approx(288_780_776, rel=1e-3)
+    assert 0.0 < bench.mfma_busy_from_profile() < 1.0
