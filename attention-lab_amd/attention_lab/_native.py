@@ -15,7 +15,7 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
 SELECT_STATE_WORDS = 2112
@@ -34,6 +34,8 @@ SIGNATURES = {
     "attnlab_score_grouped": (_i, [_p] * 8 + [_i64] + [_i] * 10 + [_p, _p]),
     "attnlab_score_prologue": (_i, [_p] * 6 + [_i] * 7 + [_p]),
     "attnlab_project_keys": (_i, [_p, _i64, _i64, _p, _p] + [_i] * 7 + [_p]),
+    "attnlab_score_grouped_f32": (_i, [_p] * 8 + [_i64] + [_i] * 9 + [_p, _p]),
+    "attnlab_project_keys_f32": (_i, [_p, _i64, _i64, _p, _p] + [_i] * 7 + [_p]),
     "attnlab_score_lightning": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 8 + [_p]),
     "attnlab_score_lightning_batched": (_i, [_p, _i, _p, _p, _p, _i64] + [_i] * 10 + [_p]),
     "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
@@ -45,6 +47,7 @@ SIGNATURES = {
     "attnlab_prefill_attend": (_i, [_p, _p, _p, _i64, _i, _p] + [_i] * 8 + [_f, _p]),
     "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
     "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
+    "attnlab_sparse_decode_step_f32": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

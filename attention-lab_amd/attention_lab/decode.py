@@ -13,7 +13,8 @@ module is a drop-in for it; the torch ops under each function are replaced by th
 
 The `backend` arguments are validated as in the reference and otherwise ignored: the HIP kernels are the backend.
 The selection tie order is defined (equal scores: lower position first) where torch.topk leaves it open. Only
-bfloat16 caches and index tables with head_dim 128 and T == 1 run here; other inputs raise ValueError.
+bfloat16 K/V caches with head_dim 128 and T == 1 run here, over a bfloat16 index table or a trained bank's float32
+one (trained.py:78-81); other inputs raise ValueError.
 """
 from __future__ import annotations
 
@@ -193,10 +194,15 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     B, G, h, T, d = q_main.shape
     if T != 1:
         raise ValueError("a decode step takes exactly one new query position")
-    for t, n in ((q_main, "q_main"), (q_pre, "q_pre"), (k_cache, "k_cache"), (v_cache, "v_cache"), (zT, "zT"),
-                 (wq_t_scaled, "wq_t_scaled"), (wk, "wk")):
-        if t.dtype != torch.bfloat16:
-            raise ValueError(f"{n} must be bfloat16 on the HIP path, got {t.dtype}")
+    # the index side is bfloat16, or float32 throughout for a trained bank (trained.py:78-81)
+    idx_dt = zT.dtype
+    if idx_dt not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"zT must be bfloat16 or float32, got {idx_dt}")
+    for t, n, want in ((q_main, "q_main", torch.bfloat16), (q_pre, "q_pre", idx_dt), (k_cache, "k_cache", torch.bfloat16),
+                       (v_cache, "v_cache", torch.bfloat16), (zT, "zT", idx_dt), (wq_t_scaled, "wq_t_scaled", idx_dt),
+                       (wk, "wk", idx_dt)):
+        if t.dtype != want:
+            raise ValueError(f"{n} must be {want} on the HIP path, got {t.dtype}")
         if not t.is_cuda:
             raise ValueError(f"{n} must live on a HIP device")
     if d != hip_attend.HEAD_DIM or not 1 <= h <= hip_attend.MAX_H:
@@ -221,8 +227,8 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     q_cat = q_pre.reshape(B, G, h * d).contiguous()
     k_new = None
     if k_pre_new is not None:
-        if tuple(k_pre_new.shape) != (B, G, 1, d) or k_pre_new.dtype != torch.bfloat16:
-            raise ValueError("k_pre_new must be a bfloat16 [B, G, 1, d] tensor")
+        if tuple(k_pre_new.shape) != (B, G, 1, d) or k_pre_new.dtype != idx_dt:
+            raise ValueError(f"k_pre_new must be a {idx_dt} [B, G, 1, d] tensor")
         k_new = k_pre_new.reshape(B, G, d).contiguous()
         wc = int(write_col) if write_col >= 0 else C + int(write_col)
         if not 0 <= wc < C or lo <= wc < hi:
@@ -238,7 +244,8 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     state = _STEP_WS.bytes(k_cache.device, B * G * nat.SELECT_STATE_WORDS * 4, "state")
     out = torch.empty(B, G, h, d, dtype=torch.bfloat16, device=k_cache.device)
     flat = torch.empty(B * G * S, dtype=torch.int64, device=k_cache.device) if return_rows else None
-    nat.call("attnlab_sparse_decode_step", q.data_ptr(), q_cat.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+    entry = "attnlab_sparse_decode_step" if idx_dt == torch.bfloat16 else "attnlab_sparse_decode_step_f32"
+    nat.call(entry, q.data_ptr(), q_cat.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
              zT.data_ptr(), wq_t_scaled.contiguous().data_ptr(), wk.contiguous().data_ptr(), nat.ptr(k_new), B, G, h, r,
              C, lo, hi, legal, k, wc, sc, order, P, state.data_ptr(), ws.data_ptr(), ws.numel(), None, nat.ptr(flat),
              out.data_ptr(), nat.stream_of(k_cache.device))

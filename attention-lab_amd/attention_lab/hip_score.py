@@ -123,28 +123,31 @@ def model_views(zT4, k_pre_new4, q_pre5, indexer):
 # batched ops
 # ---------------------------------------------------------------------------------------------------------------------
 def _check_batched(zT, wk, q_cat, wq_t, k_new, u):
-    if zT.dim() != 4 or zT.dtype != torch.bfloat16 or not zT.is_contiguous() or not zT.is_cuda:
-        raise ValueError("zT must be a contiguous bfloat16 [B, G, r, C] tensor on a HIP device")
+    """Shapes of the batched score. The index table and its inputs are all bfloat16 (the reference's random indexers)
+    or all float32 (a trained bank's table, trained.py:78-81)."""
+    if zT.dim() != 4 or zT.dtype not in (torch.bfloat16, torch.float32) or not zT.is_contiguous() or not zT.is_cuda:
+        raise ValueError("zT must be a contiguous bfloat16 or float32 [B, G, r, C] tensor on a HIP device")
+    dt = zT.dtype
+    name = "bfloat16" if dt == torch.bfloat16 else "float32"
     B, G, r, C = zT.shape
     if r > MAX_R:
         raise ValueError(f"index width {r} exceeds the kernel's {MAX_R}")
     d = 0
     if k_new is not None:
-        if wk is None or wk.dtype != torch.bfloat16 or not wk.is_contiguous() or wk.dim() != 3 \
-                or tuple(wk.shape[:2]) != (G, r):
-            raise ValueError("writing the z column needs wk, a contiguous bfloat16 [G, r, d] tensor")
+        if wk is None or wk.dtype != dt or not wk.is_contiguous() or wk.dim() != 3 or tuple(wk.shape[:2]) != (G, r):
+            raise ValueError(f"writing the z column needs wk, a contiguous {name} [G, r, d] tensor")
         d = int(wk.shape[2])
-        if tuple(k_new.shape) != (B, G, d) or k_new.dtype != torch.bfloat16 or not k_new.is_contiguous():
-            raise ValueError("k_new must be a contiguous bfloat16 [B, G, d] tensor")
+        if tuple(k_new.shape) != (B, G, d) or k_new.dtype != dt or not k_new.is_contiguous():
+            raise ValueError(f"k_new must be a contiguous {name} [B, G, d] tensor")
         _on_device(k_new, zT, "k_new")
         _on_device(wk, zT, "wk")
     if u is None:
-        if q_cat is None or q_cat.dim() != 3 or tuple(q_cat.shape[:2]) != (B, G) or q_cat.dtype != torch.bfloat16 \
+        if q_cat is None or q_cat.dim() != 3 or tuple(q_cat.shape[:2]) != (B, G) or q_cat.dtype != dt \
                 or not q_cat.is_contiguous():
-            raise ValueError("q_cat must be a contiguous bfloat16 [B, G, hd] tensor")
+            raise ValueError(f"q_cat must be a contiguous {name} [B, G, hd] tensor")
         hd = int(q_cat.shape[2])
-        if wq_t is None or tuple(wq_t.shape) != (G, hd, r) or wq_t.dtype != torch.bfloat16 or not wq_t.is_contiguous():
-            raise ValueError("wq_t must be a contiguous bfloat16 [G, hd, r] tensor")
+        if wq_t is None or tuple(wq_t.shape) != (G, hd, r) or wq_t.dtype != dt or not wq_t.is_contiguous():
+            raise ValueError(f"wq_t must be a contiguous {name} [G, hd, r] tensor")
         for t, n in ((q_cat, "q_cat"), (wq_t, "wq_t")):
             _on_device(t, zT, n)
     else:
@@ -159,7 +162,8 @@ def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=Non
                   out=None, u_out=None, state=None):
     """Batched parity-mode score: optional z-column write of k_new, u from (q_cat, wq_t) or given, scan of [lo, hi).
 
-    zT [B,G,r,C] bf16; q_cat [B,G,hd]; wq_t [G,hd,r]; u [B,G,r] fp32; k_new [B,G,d]. Returns fp32 [B, G, hi-lo].
+    zT [B,G,r,C] bf16, or float32 for a trained bank (then q_cat, wq_t, wk and k_new are float32 too); q_cat [B,G,hd];
+    wq_t [G,hd,r]; u [B,G,r] fp32; k_new [B,G,d]. Returns fp32 [B, G, hi-lo].
     state: optional zeroed int32 select state [B, G, SELECT_STATE_WORDS] that receives the scores' first-digit
     histogram for select_rows.
     """
@@ -178,6 +182,13 @@ def score_grouped(zT, lo: int, hi: int, *, wk=None, q_cat=None, wq_t=None, u=Non
     if u_out is not None and (u_out.dtype != torch.float32 or tuple(u_out.shape) != (B, G, r) or not u_out.is_contiguous()):
         raise ValueError("u_out must be a contiguous float32 [B, G, r] tensor")
     check_state(state, B, G, zT.device)
+    if zT.dtype == torch.float32:
+        if u is None and u_out is None and M > 0:
+            u_out = torch.empty(B, G, r, dtype=torch.float32, device=zT.device)
+        nat.call("attnlab_score_grouped_f32", zT.data_ptr(), nat.ptr(k_new), nat.ptr(wk), nat.ptr(q_cat),
+                 nat.ptr(wq_t), nat.ptr(u), nat.ptr(u_out), out.data_ptr(), out.shape[2], B, G, r, C, d, hd, lo, hi,
+                 write_col if k_new is not None else 0, nat.ptr(state), nat.stream_of(zT.device))
+        return out[..., :M]
     nat.call("attnlab_score_grouped", zT.data_ptr(), nat.ptr(k_new), nat.ptr(wk), nat.ptr(q_cat), nat.ptr(wq_t),
              nat.ptr(u), nat.ptr(u_out), out.data_ptr(), out.shape[2], B, G, r, C, d, hd, lo, hi,
              write_col if k_new is not None else 0, 1, nat.ptr(state), nat.stream_of(zT.device))
@@ -196,14 +207,23 @@ def project_queries(q_pre, wq_t_scaled):
     B, G, h, T, d = q_pre.shape
     if T != 1:
         raise ValueError("the HIP projection takes one query position")
-    if q_pre.dtype != torch.bfloat16 or wq_t_scaled.dtype != torch.bfloat16:
-        raise ValueError("q_pre and wq_t_scaled must be bfloat16")
+    dt = q_pre.dtype
+    if dt not in (torch.bfloat16, torch.float32) or wq_t_scaled.dtype != dt:
+        raise ValueError("q_pre and wq_t_scaled must both be bfloat16, or both float32 (a trained bank)")
+    if not q_pre.is_cuda or wq_t_scaled.device != q_pre.device:
+        raise ValueError("q_pre and wq_t_scaled must live on one HIP device")
     r = int(wq_t_scaled.shape[2])
+    if r > MAX_R or tuple(wq_t_scaled.shape) != (G, h * d, r):
+        raise ValueError(f"wq_t_scaled must be [G, h*d, r <= {MAX_R}]")
     q_cat = q_pre.reshape(B, G, h * d).contiguous()
     u = torch.empty(B, G, r, dtype=torch.float32, device=q_pre.device)
     wq = wq_t_scaled.contiguous()
-    nat.call("attnlab_score_prologue", None, None, None, q_cat.data_ptr(), wq.data_ptr(), u.data_ptr(), B, G, r, 0,
-             d, h * d, 0, nat.stream_of(q_pre.device))
+    if dt == torch.float32:   # the fp32 score entry with no table and no candidates is the projection alone
+        nat.call("attnlab_score_grouped_f32", None, None, None, q_cat.data_ptr(), wq.data_ptr(), None, u.data_ptr(),
+                 None, 0, B, G, r, 0, d, h * d, 0, 0, 0, None, nat.stream_of(q_pre.device))
+    else:
+        nat.call("attnlab_score_prologue", None, None, None, q_cat.data_ptr(), wq.data_ptr(), u.data_ptr(), B, G, r,
+                 0, d, h * d, 0, nat.stream_of(q_pre.device))
     return u.view(B, G, 1, r)
 
 

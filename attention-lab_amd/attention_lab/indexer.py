@@ -25,23 +25,26 @@ def project_keys(k_pre: torch.Tensor, wk: torch.Tensor, *, out=None, col0: int =
     B, G, T, d = k_pre.shape
     if wk.shape[0] != G or wk.shape[2] != d:
         raise ValueError(f"wk {tuple(wk.shape)} does not match k_pre {tuple(k_pre.shape)}")
-    if k_pre.dtype != torch.bfloat16 or wk.dtype != torch.bfloat16 or not k_pre.is_cuda or wk.device != k_pre.device:
-        raise ValueError("k_pre and wk must be bfloat16 on one HIP device")
+    dt = wk.dtype
+    if dt not in (torch.bfloat16, torch.float32) or k_pre.dtype != dt or not k_pre.is_cuda or wk.device != k_pre.device:
+        raise ValueError("k_pre and wk must both be bfloat16 (or both float32, a trained bank) on one HIP device")
+    align = 8 if dt == torch.bfloat16 else 4   # elements per 16 bytes
     r = int(wk.shape[1])
     bg_stride = k_pre.stride(1) if G > 1 else k_pre.stride(0)
-    strided_ok = (k_pre.stride(3) == 1 and (B == 1 or k_pre.stride(0) == G * bg_stride) and bg_stride % 8 == 0
-                  and k_pre.stride(2) % 8 == 0 and k_pre.data_ptr() % 16 == 0)
+    strided_ok = (k_pre.stride(3) == 1 and (B == 1 or k_pre.stride(0) == G * bg_stride) and bg_stride % align == 0
+                  and k_pre.stride(2) % align == 0 and k_pre.data_ptr() % 16 == 0)
     if not strided_ok:
         k_pre = k_pre.contiguous()
         bg_stride = T * d
     if out is None:
-        out = torch.empty(B, G, r, T, dtype=torch.bfloat16, device=k_pre.device)
+        out = torch.empty(B, G, r, T, dtype=dt, device=k_pre.device)
         col0 = 0
-    elif out.dim() != 4 or tuple(out.shape[:3]) != (B, G, r) or out.dtype != torch.bfloat16 or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous bfloat16 [{B}, {G}, {r}, C] table")
+    elif out.dim() != 4 or tuple(out.shape[:3]) != (B, G, r) or out.dtype != dt or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {dt} [{B}, {G}, {r}, C] table")
     wkc = wk.contiguous()
-    nat.call("attnlab_project_keys", k_pre.data_ptr(), bg_stride, k_pre.stride(2), wkc.data_ptr(), out.data_ptr(), B, G,
-             T, r, d, int(out.shape[3]), int(col0), nat.stream_of(k_pre.device))
+    entry = "attnlab_project_keys" if dt == torch.bfloat16 else "attnlab_project_keys_f32"
+    nat.call(entry, k_pre.data_ptr(), bg_stride, k_pre.stride(2), wkc.data_ptr(), out.data_ptr(), B, G, T, r, d,
+             int(out.shape[3]), int(col0), nat.stream_of(k_pre.device))
     return out
 
 

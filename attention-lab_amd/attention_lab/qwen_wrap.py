@@ -13,7 +13,8 @@ embeddings, MLP, norms and lm_head are the installed model's, untouched. What ru
 - prefill: `full.full_attention` over the chunk's queries (one dense-decode launch per query position, causal) and
   the index table filled by `attnlab_project_keys`.
 
-The cache must be bfloat16 with head_dim 128 and r <= 32 (what the kernels take); anything else raises from the op.
+The K/V cache must be bfloat16 with head_dim 128 and r <= 32 (what the kernels take); the index table is bfloat16,
+or float32 for a trained bank (trained.py:78-81). Anything else raises from the op.
 
 Per layer, as in the reference (its docs/IMPLEMENTATION.md §1): hidden -> q/k/v_proj -> q_norm / k_norm -> (q_pre,
 k_pre, index features before RoPE) -> RoPE -> (q_main, k_main) -> append k_main, v (and z = Wk.k_pre) exactly once ->

@@ -42,12 +42,15 @@ extern "C" int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, 
     return layout_of(B, G, h, lo, hi, legal, k, P).total;
 }
 
-extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K,
-                                          const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
-                                          const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
-                                          int legal, int k, int write_col, float scale, int order, int P,
-                                          uint32_t* state, void* workspace, int64_t workspace_bytes,
-                                          int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+namespace {
+
+// The launches of one step after the argument checks; score(ws_u, scores, stride, state) runs the score stage for the
+// index table's dtype.
+template <typename Score>
+int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uint16_t* V, bool has_k_new, int B,
+                            int G, int h, int C, int lo, int hi, int legal, int k, float scale, int order, int P,
+                            uint32_t* state, void* workspace, int64_t workspace_bytes, int32_t* rows_out,
+                            int64_t* rows_flat, uint16_t* out, void* stream, Score score) {
     using namespace attnlab;
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
@@ -68,14 +71,11 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     const int d = 128;
     int rc;
     if (k > 0) {
-        // u_out in the workspace selects the two-launch score: u and the z column once per (b, g), then the scan
-        rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, reinterpret_cast<float*>(ws + L.u), scores,
-                                L.score_stride, B, G, r, C, d,
-                                h * d, lo, hi, write_col, 1, state, s);
-    } else if (k_new) {
+        // u goes to the workspace (the score kernels that build it in-kernel also store it there)
+        rc = score(reinterpret_cast<float*>(ws + L.u), scores, L.score_stride, lo, hi, state, s);
+    } else if (has_k_new) {
         // no candidate is read this step, but the newest key still gets its index column (empty scan range)
-        rc = score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, nullptr, nullptr, 0, B, G, r, C, d, h * d, lo, lo,
-                                write_col, 1, nullptr, s);
+        rc = score(nullptr, nullptr, 0, lo, lo, nullptr, s);
     } else {
         rc = ATTNLAB_OK;
     }
@@ -84,4 +84,36 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
                           k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
     if (rc) return rc;
     return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
+}
+
+}  // namespace
+
+extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K,
+                                          const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
+                                          const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
+                                          int legal, int k, int write_col, float scale, int order, int P,
+                                          uint32_t* state, void* workspace, int64_t workspace_bytes,
+                                          int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+    return sparse_decode_step_impl(
+        q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
+        workspace_bytes, rows_out, rows_flat, out, stream,
+        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, hipStream_t s) {
+            return attnlab::score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r, C,
+                                               128, h * 128, slo, shi, write_col, 1, st, s);
+        });
+}
+
+extern "C" int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const float* q_cat, const uint16_t* K,
+                                              const uint16_t* V, float* zT, const float* wq_t, const float* wk,
+                                              const float* k_new, int B, int G, int h, int r, int C, int lo, int hi,
+                                              int legal, int k, int write_col, float scale, int order, int P,
+                                              uint32_t* state, void* workspace, int64_t workspace_bytes,
+                                              int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
+    return sparse_decode_step_impl(
+        q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
+        workspace_bytes, rows_out, rows_flat, out, stream,
+        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, hipStream_t s) {
+            return attnlab::score_grouped_f32_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r,
+                                                   C, 128, h * 128, slo, shi, write_col, st, s);
+        });
 }

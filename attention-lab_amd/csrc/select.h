@@ -70,4 +70,9 @@ int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, 
                        int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector, uint32_t* hist,
                        hipStream_t stream);
 
+// attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
+int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,
+                           const float* u_in, float* u_out, float* out, int64_t out_stride, int B, int G, int r,
+                           int C, int d, int hd, int lo, int hi, int write_col, uint32_t* hist, hipStream_t stream);
+
 }  // namespace attnlab

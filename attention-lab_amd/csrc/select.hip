@@ -171,14 +171,83 @@ __device__ __forceinline__ uint32_t radix_threshold(int k, int M, ForEach for_ea
     return prefix;
 }
 
-// Score order: fill sortbuf[0, next_pow2(k)) with 0, below every staged (key, ~index) pair (~index > 0 for any
+// Length of the score-order sort: k rounded up to a power of two, at least one 128-element chunk.
+__device__ __forceinline__ int sort_len(int k) {
+    int n = 128;
+    while (n < k) n <<= 1;
+    return n;
+}
+
+// Score order: fill sortbuf[0, sort_len(k)) with 0, below every staged (key, ~index) pair (~index > 0 for any
 // index < 2^32 - 1), so the padding sorts last. Ordered before the emission by the barriers of the block scan that
 // follows.
 __device__ __forceinline__ void init_sortbuf(const SelectArgs& a, SelectShared& sh) {
     if (a.order != ATTNLAB_ORDER_SCORE) return;
-    int n = 1;
-    while (n < a.k) n <<= 1;
+    const int n = sort_len(a.k);
     for (int i = threadIdx.x; i < n; i += kSelThreads) sh.sortbuf[i] = 0ull;
+}
+
+// Bitonic sort of buf[0, n), descending, n a power of two >= 128. Every compare-exchange whose partner lies in the same
+// 128-element chunk runs in registers: a wave holds a chunk as two elements per lane (c0 + lane, c0 + 64 + lane), so
+// stride 64 is within a lane and strides 32..1 are lane shuffles. Only strides >= 128 go through LDS, one barrier
+// each; a chunk pass runs every stride of a merge below 128 (and, first, every merge up to 128) with one barrier.
+__device__ __forceinline__ void cmpx_reg(uint64_t& x, int i, int stride, int size, int lane) {
+    const uint64_t y = __shfl_xor(x, stride);
+    const bool lower = (lane & stride) == 0;
+    const bool desc = (i & size) == 0;
+    // the lower element of a pair keeps the larger value in a descending block
+    const bool take_max = lower == desc;
+    x = take_max ? (x > y ? x : y) : (x < y ? x : y);
+}
+
+__device__ __forceinline__ void chunk_pass(uint64_t* buf, int n, int size_first, int size_last, int stride_first) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kWaves = kSelThreads / 64;
+    for (int c0 = wave * 128; c0 < n; c0 += kWaves * 128) {
+        uint64_t x0 = buf[c0 + lane], x1 = buf[c0 + 64 + lane];
+        const int i0 = c0 + lane, i1 = c0 + 64 + lane;
+        for (int size = size_first; size <= size_last; size <<= 1) {
+            int stride = size == size_first ? stride_first : size >> 1;
+            if (stride == 64) {
+                const bool desc = (i0 & size) == 0;
+                if ((x0 < x1) == desc) {
+                    const uint64_t t = x0;
+                    x0 = x1;
+                    x1 = t;
+                }
+                stride = 32;
+            }
+            for (; stride > 0; stride >>= 1) {
+                cmpx_reg(x0, i0, stride, size, lane);
+                cmpx_reg(x1, i1, stride, size, lane);
+            }
+        }
+        buf[c0 + lane] = x0;
+        buf[c0 + 64 + lane] = x1;
+    }
+}
+
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t* buf, int n) {
+    const int tid = threadIdx.x;
+    chunk_pass(buf, n, 2, 128, 1);   // every merge up to size 128, inside the chunks
+    __syncthreads();
+    for (int size = 256; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride >= 128; stride >>= 1) {
+            for (int i = tid; i < n / 2; i += kSelThreads) {
+                const int lo_i = 2 * i - (i & (stride - 1));
+                const int hi_i = lo_i + stride;
+                const bool desc = (lo_i & size) == 0;
+                const uint64_t x = buf[lo_i], y = buf[hi_i];
+                if ((x < y) == desc) {
+                    buf[lo_i] = y;
+                    buf[hi_i] = x;
+                }
+            }
+            __syncthreads();
+        }
+        chunk_pass(buf, n, size, size, 64);
+        __syncthreads();
+    }
 }
 
 // F positions and, in score order, the sorted candidates (the selected pairs are staged in sh.sortbuf).
@@ -200,26 +269,10 @@ __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectS
         }
     }
     if (order != ATTNLAB_ORDER_SCORE || k == 0) return;
-    // bitonic sort, descending on (key, ~index): larger score first, then lower index (sortbuf[0, n) was pre-filled
-    // by init_sortbuf before the emission)
-    int n = 1;
-    while (n < k) n <<= 1;
+    // descending on (key, ~index): larger score first, then lower index (sortbuf[0, sort_len(k)) was pre-filled by
+    // init_sortbuf before the emission)
     __syncthreads();
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < n / 2; i += kSelThreads) {
-                const int lo_i = 2 * i - (i & (stride - 1));
-                const int hi_i = lo_i + stride;
-                const bool desc = ((lo_i & size) == 0);
-                const uint64_t x = sh.sortbuf[lo_i], y = sh.sortbuf[hi_i];
-                if ((x < y) == desc) {
-                    sh.sortbuf[lo_i] = y;
-                    sh.sortbuf[hi_i] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
+    bitonic_sort_desc(sh.sortbuf, sort_len(k));
     const float* srow = a.scores + (size_t)row * a.score_stride;
     int32_t* ti = a.top_idx ? a.top_idx + (size_t)row * a.top_stride : nullptr;
     float* tv = a.top_val ? a.top_val + (size_t)row * a.top_stride : nullptr;

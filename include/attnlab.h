@@ -94,6 +94,31 @@ int attnlab_project_keys(const uint16_t* k_pre, int64_t k_bg_stride, int64_t k_r
                          uint16_t* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream);
 
 /*
+ * Float32 index tables (a trained bank's cache: FrozenIndexer keeps wq/wk in float32, trained.py:11-18, and the
+ * state's cache is built with index_dtype=float32, trained.py:78-81; FrozenBank.guard refuses anything else,
+ * trained.py:45-46). The same contract as attnlab_score_grouped with every index-side operand in fp32:
+ *   if k_new != NULL:  zT[b,g,j,write_col] = sum_e wk[g,j,e] * k_new[b,g,e]   (fp32, no rounding to bf16)
+ *   u[j] = sum_f q_cat[b,g,f] * wq_t[g,f,j]   or u_in;   out[b,g,m] = sum_j u[j] * zT[b,g,j,lo+m]
+ * zT: [B,G,r,C] fp32 (16-byte loads when C % 4 == 0 and zT is 16-byte aligned, 4-byte loads otherwise);
+ * k_new [B,G,d], wk [G,r,d], q_cat [B,G,hd],
+ * wq_t [G,hd,r] fp32. u_out, when given without u_in, receives u (q_cat and wq_t required); the scan of hi > lo
+ * reads u from u_in or u_out, so one of them is required then. A call with k_new == NULL and lo == hi is a pure query
+ * projection (project_queries, indexer.py:20-24) and may pass zT == NULL, C == 0. No vector flag: the load width
+ * follows the table's alignment. state as in attnlab_score_grouped.
+ */
+int attnlab_score_grouped_f32(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,
+                              const float* u_in, float* u_out, float* out, int64_t out_stride, int B, int G, int r,
+                              int C, int d, int hd, int lo, int hi, int write_col, uint32_t* state, void* stream);
+
+/*
+ * Bulk fp32 index-table build (project_keys, indexer.py:15-17, on a float32 cache): zT[b,g,j,col0+t] =
+ * sum_e wk[g,j,e] * k_pre[b,g,t,e] in fp32. k_pre rows 16-byte aligned (strides in elements, multiples of 4),
+ * d % 4 == 0, d <= 128. zT: [B,G,r,C] fp32. Requires 0 <= col0, col0 + T <= C.
+ */
+int attnlab_project_keys_f32(const float* k_pre, int64_t k_bg_stride, int64_t k_row_stride, const float* wk,
+                             float* zT, int B, int G, int T, int r, int d, int C, int col0, void* stream);
+
+/*
  * Lightning-indexer score (no reference kernel: the generalisation north_star names; the grouped score of
  * indexer.py:27-29 is the special case nh=1, w=1, relu=0, keys transposed):
  *   out[b,kg,t] = sum_i w[b,kg,i] * act(sum_j q[b,kg,i,j] * key[b,kg,t,j])   for t in [lo, hi), act = ReLU or identity
@@ -225,6 +250,18 @@ int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, co
                                float scale, int order, int P, uint32_t* state, void* workspace,
                                int64_t workspace_bytes, int32_t* rows_out, int64_t* rows_flat, uint16_t* out,
                                void* stream);
+
+/*
+ * attnlab_sparse_decode_step over a float32 index table (sparse_decode_step_kernel, decode.py:145-163, with a trained
+ * bank's fp32 wq_t_scaled/wk and fp32 z cache, trained.py:78-81): q_cat [B,G,h*128], zT [B,G,r,C],
+ * wq_t [G,h*128,r], wk [G,r,128] and k_new [B,G,128] are fp32; q_main, K, V and out stay bf16. Same workspace size
+ * (attnlab_sparse_decode_workspace), state, order and row-list contract.
+ */
+int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const float* q_cat, const uint16_t* K, const uint16_t* V,
+                                   float* zT, const float* wq_t, const float* wk, const float* k_new, int B, int G,
+                                   int h, int r, int C, int lo, int hi, int legal, int k, int write_col, float scale,
+                                   int order, int P, uint32_t* state, void* workspace, int64_t workspace_bytes,
+                                   int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }
