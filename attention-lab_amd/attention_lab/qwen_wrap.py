@@ -44,10 +44,12 @@ except ImportError as _e:  # pragma: no cover
 MASK_BYPASS = {"full_attention": None}
 
 SELECTORS = ("index", "recent", "uniform")   # D0 / B / C
+SLOT_ALIGN = 8   # cache rows per (b, g) are allocated in multiples of this (16 bytes of a bf16 index-table row)
 
 
 class LabCache:
-    """Per-layer K/V [B,G,C,d] and optional index tables zT [B,G,r,C], one legal length shared by all layers.
+    """Per-layer K/V [B,G,C,d] and optional index tables zT [B,G,r,C], one legal length shared by all layers. In memory
+    C is `slots`, the capacity rounded up to a multiple of SLOT_ALIGN; positions at or past `capacity` are never used.
 
     Allocated with torch.empty: slots at or beyond valid_length hold garbage (tests poison them with NaN) and no read
     or selection may touch them.
@@ -59,17 +61,21 @@ class LabCache:
             raise ValueError("capacity and layers must be positive")
         self.layers, self.batch, self.groups = int(layers), int(batch), int(groups)
         self.capacity, self.head_dim = int(capacity), int(head_dim)
+        # rows per (b, g) in memory: the capacity rounded up to a multiple of SLOT_ALIGN, so every index-table row
+        # starts 16 bytes aligned and the score kernels take their 16-byte loads whatever the capacity; the slots
+        # past `capacity` are never written or read
+        self.slots = -(-self.capacity // SLOT_ALIGN) * SLOT_ALIGN
         self.index_dim = None if index_dim is None else int(index_dim)
         self.device, self.dtype = torch.device(device), dtype
         self.index_dtype = dtype if index_dtype is None else index_dtype
-        shape = (self.batch, self.groups, self.capacity, self.head_dim)
+        shape = (self.batch, self.groups, self.slots, self.head_dim)
         self.k = [torch.empty(shape, device=self.device, dtype=dtype) for _ in range(self.layers)]
         self.v = [torch.empty(shape, device=self.device, dtype=dtype) for _ in range(self.layers)]
         self.z = None if self.index_dim is None else [
-            torch.empty(self.batch, self.groups, self.index_dim, self.capacity, device=self.device, dtype=self.index_dtype)
+            torch.empty(self.batch, self.groups, self.index_dim, self.slots, device=self.device, dtype=self.index_dtype)
             for _ in range(self.layers)]
         self.valid_length = 0
-        self.offsets = row_offsets(self.batch, self.groups, self.capacity, self.device)      # [B,G,1]
+        self.offsets = row_offsets(self.batch, self.groups, self.slots, self.device)         # [B,G,1]
         self.prefix_rows = (torch.arange(FIXED_PREFIX, device=self.device).view(1, 1, -1) + self.offsets).contiguous()
         self.recent_base = (torch.arange(-FIXED_RECENT, 0, device=self.device).view(1, 1, -1)
                             + self.offsets).contiguous()
@@ -129,9 +135,9 @@ class LabCache:
         return new
 
     def bytes(self) -> dict:
-        kv = self.layers * 2 * self.batch * self.groups * self.capacity * self.head_dim * self.k[0].element_size()
-        z = 0 if self.z is None else (self.layers * self.batch * self.groups * self.index_dim * self.capacity
-                                      * self.z[0].element_size())
+        """Bytes the cache holds (its tensors, padding slots included)."""
+        kv = sum(t.numel() * t.element_size() for t in self.k + self.v)
+        z = 0 if self.z is None else sum(t.numel() * t.element_size() for t in self.z)
         return {"kv_bytes": kv, "index_bytes": z, "total_bytes": kv + z}
 
 

@@ -73,6 +73,15 @@ def parse_args():
                          "the sparse read (rho = 1/32); per-step logits compared, one JSON line")
     ap.add_argument("--c4-steps", type=int, default=128)
     ap.add_argument("--c4-prompt", type=int, default=8192)
+    ap.add_argument("--c5", action="store_true",
+                    help="instead of the bench line: BASELINE configs[4], a random-init Qwen3-8B-shaped model read "
+                         "through the wrapper at batch 16 x 32K context (uniform random ids): 64 greedy steps on the "
+                         "full read, the same tokens on the sparse read (rho = 1/32), eager per-step times; one JSON "
+                         "line")
+    ap.add_argument("--c5-steps", type=int, default=64)
+    ap.add_argument("--c5-context", type=int, default=32768)
+    ap.add_argument("--c5-batch", type=int, default=16)
+    ap.add_argument("--c5-chunk", type=int, default=2048, help="prefill chunk of the configs[4] run")
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
@@ -577,6 +586,152 @@ def qwen3_1p7b(torch, dev, seed):
     return model
 
 
+def qwen3_8b(torch, dev, seed):
+    """BASELINE configs[4]'s model shape (36 layers, hidden 4096, 32q/8kv, d=128, FFN 12288, vocab 151936) with random
+    bf16 weights ~ N(0, 0.02) (transformers' own init), on `dev`."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=40960,
+                      rope_theta=1_000_000.0, rms_norm_eps=1e-6, tie_word_embeddings=False, initializer_range=0.02,
+                      attn_implementation="sdpa")
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = Qwen3ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    for p in model.parameters():
+        p.requires_grad_(False)
+    torch.cuda.empty_cache()
+    return model
+
+
+def logit_agreement(torch, a, b):
+    """a, b: [n, V] float32 logits of the same positions."""
+    lp, lq = torch.log_softmax(b, -1), torch.log_softmax(a, -1)
+    return {"top1_agreement": float((a.argmax(-1) == b.argmax(-1)).float().mean()),
+            "max_abs_diff": float((a - b).abs().max()),
+            "rel_norm_diff": float((a - b).norm() / b.norm()),
+            "kl_mean": float((lp.exp() * (lp - lq)).sum(-1).mean())}
+
+
+def run_c5(torch, dev, args):
+    """configs[4] through the wrapper on the HIP kernels: one chunked prefill of B x L uniform random ids (index table
+    built on the way), greedy decode on the full read (A), rollback, the same tokens (teacher-forced) on the sparse
+    read (D0, rho = 1/32), and a few steps with k0 = capacity (every candidate selected, which must equal A). Per-step
+    times are eager wall clock (the model's own layers launch from Python), each step ending in a synchronize."""
+    from attention_lab.qwen_wrap import LabRunner, LabState, make_state, wrap_model
+    B, L, steps, chunk = args.c5_batch, args.c5_context, args.c5_steps, args.c5_chunk
+    t_setup = time.perf_counter()
+    model = qwen3_8b(torch, dev, args.seed)
+    holder = wrap_model(model)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    prompt = torch.randint(0, model.config.vocab_size, (B, L), device=dev, generator=gen)
+    cap = L + steps + 1
+    print(f"[c5] model ready in {time.perf_counter() - t_setup:.1f}s", file=sys.stderr, flush=True)
+    res = {}
+    with torch.inference_mode():
+        sparse = make_state(model, cap, "sparse", selector="index", r=32, seed=args.seed, batch=B)
+        cache = sparse.cache
+        res["cache_gb"] = round(cache.bytes()["total_bytes"] / 1e9, 2)
+        runner = LabRunner(model, holder, sparse)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = None
+        seg = max(chunk, L // 8)
+        for a in range(0, L, seg):
+            logits = runner.prefill(prompt[:, a:a + seg], chunk)
+            torch.cuda.synchronize()
+            print(f"[c5] prefill {a + prompt[:, a:a + seg].shape[1]}/{L} ({time.perf_counter() - t0:.1f}s)",
+                  file=sys.stderr, flush=True)
+        res["prefill_s"] = round(time.perf_counter() - t0, 2)
+        res["prefill_tok_s"] = round(B * L / res["prefill_s"], 1)
+        first = logits[:, -1].argmax(-1, keepdim=True)
+
+        def decode(run, feed, n):
+            """n steps; feed(i, last_logits) -> token ids [B, 1]; returns ([n, B, V] logits, tokens, ms per step)."""
+            outs, toks, times = [], [], []
+            lg = None
+            for i in range(n):
+                tok = feed(i, lg)
+                toks.append(tok)
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                lg = run.step(tok)[:, -1].float()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t)
+                outs.append(lg)
+            warm = times[2:] if len(times) > 4 else times
+            return torch.stack(outs), toks, 1e3 * sum(warm) / len(warm)
+
+        full = LabRunner(model, holder, LabState(cache, sparse.indexers, mode="full"))
+        full_logits, tokens, res["decode_ms_full"] = decode(
+            full, lambda i, lg: first if i == 0 else lg.argmax(-1, keepdim=True), steps)
+        print(f"[c5] full read: {res['decode_ms_full']:.2f} ms per step", file=sys.stderr, flush=True)
+        cache.rollback(L)
+        res["k0"] = sparse.begin_request(args.rho)
+        sp_logits, _, res["decode_ms_sparse"] = decode(runner, lambda i, lg: tokens[i], steps)
+        print(f"[c5] sparse read: {res['decode_ms_sparse']:.2f} ms per step", file=sys.stderr, flush=True)
+        res["sparse_vs_full"] = logit_agreement(torch, sp_logits.flatten(0, 1), full_logits.flatten(0, 1))
+        cache.rollback(L)
+        n_all = min(4, steps)
+        allk = LabState(cache, sparse.indexers, mode="sparse", selector="index", canonical_order=True)
+        allk.begin_request(args.rho, k0=cap)
+        all_logits, _, _ = decode(LabRunner(model, holder, allk), lambda i, lg: tokens[i], n_all)
+        res["sparse_k0_capacity_vs_full"] = logit_agreement(torch, all_logits.flatten(0, 1),
+                                                            full_logits[:n_all].flatten(0, 1))
+        cache.rollback(L)
+
+        def graph_step(run, tok, reps=20):
+            """The whole-model step at legal length L + 1 captured in one HIP graph and replayed `reps` times (each
+            replay rewrites the same cache slot): GPU time per step without the eager launch overhead. Returns (ms,
+            replay output == eager output)."""
+            run.step(tok)                      # allocations and workspaces before the capture
+            cache.rollback(L)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = run.step(tok)
+            cache.rollback(L)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            got = out.clone()
+            want = run.step(tok)
+            cache.rollback(L)
+            torch.cuda.synchronize()
+            del g
+            return e0.elapsed_time(e1) / reps, bool(torch.equal(got, want))
+
+        res["graph_ms_full"], res["graph_full_equals_eager"] = graph_step(full, tokens[0])
+        res["graph_ms_sparse"], res["graph_sparse_equals_eager"] = graph_step(runner, tokens[0])
+        print(f"[c5] graph steps: full {res['graph_ms_full']:.2f} ms, sparse {res['graph_ms_sparse']:.2f} ms",
+              file=sys.stderr, flush=True)
+    res["graph_tok_s_full"] = round(B * 1e3 / res["graph_ms_full"], 1)
+    res["graph_tok_s_sparse"] = round(B * 1e3 / res["graph_ms_sparse"], 1)
+    res["graph_sparse_speedup"] = round(res["graph_ms_full"] / res["graph_ms_sparse"], 3)
+    res["tok_s_full"] = round(B * 1e3 / res["decode_ms_full"], 1)
+    res["tok_s_sparse"] = round(B * 1e3 / res["decode_ms_sparse"], 1)
+    res["sparse_speedup"] = round(res["decode_ms_full"] / res["decode_ms_sparse"], 3)
+    print(json.dumps({
+        "workload": f"configs[4]: random-init Qwen3-8B shape (36 layers, hidden 4096, 32q/8kv, d=128, FFN 12288, "
+                    f"vocab 151936, bf16 ~ N(0, 0.02)), batch {B} x {L}-token uniform random context, {steps} greedy "
+                    f"steps on the full read, the same tokens on the sparse read (rho={args.rho}, one r=32 grouped "
+                    f"indexer per layer) and {n_all} on the sparse read with k0 = capacity; whole model on the GPU, "
+                    f"attention through the HIP kernels; decode_ms_* are eager per-step wall clock (the model's layers launch from "
+                    f"Python), graph_ms_* one whole step at legal length {L} + 1 replayed from a HIP graph",
+        **res,
+        "note": "untrained indexers pick rows unrelated to the attention scores, so sparse_vs_full measures the 1/32 "
+                "read's departure, not a quality result; k0 = capacity must reproduce the full read up to bf16 "
+                "rounding and summation order",
+    }))
+    return 0
+
+
 def run_c4(torch, dev, args):
     """configs[3] through the wrapper on the HIP kernels: greedy decode on the full read (A); the same tokens on the
     sparse read (D0, rho = 1/32) and on the sparse read with k0 = capacity (every candidate selected, which must
@@ -780,6 +935,8 @@ def main() -> int:
         return run_sweeps(torch, dev, args.sweeps)
     if args.c4:
         return run_c4(torch, dev, args)
+    if args.c5:
+        return run_c5(torch, dev, args)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,

@@ -81,7 +81,8 @@ def test_clone_shares_no_storage_and_bytes_ledger():
     d.k[0].zero_()
     assert float(c.k[0][0, 0, 0, 0]) == 1.0 and d.valid_length == 1 and d.writes == c.writes
     b = c.bytes()
-    assert b["kv_bytes"] == 2 * 2 * 2 * 2 * 300 * 4 * 4 and b["index_bytes"] == 2 * 2 * 2 * 3 * 300 * 4
+    # capacity 300 is held as 304 slots per (b, g) (a multiple of 8)
+    assert b["kv_bytes"] == 2 * 2 * 2 * 2 * 304 * 4 * 4 and b["index_bytes"] == 2 * 2 * 2 * 3 * 304 * 4
     assert b["total_bytes"] == b["kv_bytes"] + b["index_bytes"]
 
 
@@ -130,4 +131,7 @@ def test_make_cache_takes_the_model_geometry():
     m = tiny_qwen3(dtype=torch.float32)
     c = make_cache(m, 50, with_index=True, index_dim=8, batch=3)
     assert (c.layers, c.batch, c.groups, c.capacity, c.head_dim, c.index_dim) == (2, 3, 2, 50, 16, 8)
-    assert c.k[0].dtype == torch.float32 and tuple(c.z[1].shape) == (3, 2, 8, 50)
+    # rows in memory: the capacity rounded up to 8 (16-byte index-table rows); the bytes count what is held
+    assert c.slots == 56 and tuple(c.k[0].shape) == (3, 2, 56, 16)
+    assert c.k[0].dtype == torch.float32 and tuple(c.z[1].shape) == (3, 2, 8, 56)
+    assert c.bytes()["total_bytes"] == sum(t.numel() * t.element_size() for t in c.k + c.v + c.z)
