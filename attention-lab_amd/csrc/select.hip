@@ -9,11 +9,12 @@
 // score of one row into 4 bins and the LDS atomics serialize). In the fused decode step the first-digit histogram is
 // built by the score kernel, which already holds every score, and arrives here in global memory; this kernel reads it
 // and clears it for the next call, so only keys that share the first digit with the threshold are touched again.
-// Each thread owns a contiguous segment of the row, so once the threshold key T and the number of ties to keep are
-// known, one block-wide exclusive scan of (count > T, count == T) gives every thread the output slot of its first
-// selected element and the rank of its first tie: indices come out in ascending order with no sort. The score order
-// (the reference's cat(F, topk) row list) sorts the k selected (key, index) pairs once in LDS. Rows up to 1024 x 32
-// scores keep their keys in registers; longer rows (L = 64K..128K) re-read the row (L2-resident) in every pass.
+// Once the threshold key T and the number of ties to keep are known, every thread owns a contiguous range of indices
+// (its segment of the row, or for register-resident rows its word of two LDS bitmaps), and one block-wide exclusive
+// scan of (count > T, count == T) gives it the output slot of its first selected element and the rank of its first
+// tie: indices come out in ascending order with no sort. The score order (the reference's cat(F, topk) row list)
+// sorts the k selected (key, index) pairs once in LDS. Rows up to 32768 scores keep their keys in registers, loaded
+// coalesced; longer rows (L = 64K..128K) re-read the row (L2-resident) in every pass.
 #include "common.h"
 #include "select.h"
 
@@ -331,61 +332,157 @@ __device__ __forceinline__ Emitter make_emitter(const SelectArgs& a, int row, Se
     return e;
 }
 
-// Keys of this thread's segment held in registers (M <= 1024 * KPT).
-template <int KPT>
+// Keys in registers (M <= 4096 * CH). Thread t holds keys 4096 c + 4 t + e (c < CH, e < 4), so every load instruction
+// of a wave reads 1 KB of the row (a lane-contiguous segment per thread makes each instruction touch 64 lines, and a
+// 32K row then takes ~5 us to reach one CU). All global loads are issued before any is used: this thread's two words
+// of the first-digit histogram, then the row. The radix passes need no order. Index order comes back through two
+// bitmaps in LDS (keys above the threshold, keys equal to it), zeroed before the first barrier: each thread ORs in its
+// non-zero 4-bit pieces (a few percent of the keys are selected, so most threads OR nothing), and thread t then owns
+// word t (keys 32 t .. 32 t + 31) for the tie rule (the first krem equal keys in index order) and the emission, with
+// one block scan.
+constexpr int kRegMaxChunks = 8;                        // M <= 32768
+constexpr int kRegWords = 4096 * kRegMaxChunks / 32;    // 1024 bitmap words, one per thread
+static_assert(kRegWords == kSelThreads, "one bitmap word per thread");
+
+template <int CH>
 __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
+    static_assert(kHistBins == 2 * kSelThreads, "two histogram words per thread");
+    static_assert(CH >= 1 && CH <= kRegMaxChunks, "chunks of 4096 keys");
+    constexpr int KPT = 4 * CH;
     __shared__ SelectShared sh;
+    __shared__ __attribute__((aligned(16))) uint32_t hist2[2048];
+    __shared__ __attribute__((aligned(16))) uint32_t hist3[1024];
+    __shared__ uint32_t gtbits[kRegWords];
+    __shared__ uint32_t eqbits[kRegWords];
     const int row = xcd_contiguous_block();   // the XCD whose L2 holds the row's scores after the scan
     const int tid = threadIdx.x;
     const float* s = a.scores + (size_t)row * a.score_stride;
     const int M = a.M;
-    const int seg = tid * KPT;
-    const int nvalid = max(0, min(KPT, M - seg));
     uint32_t* ghist = a.hist ? a.hist + (size_t)row * kSelectStateWords : nullptr;
-    uint32_t key[KPT];
-    const bool vec = ((reinterpret_cast<uintptr_t>(s) & 15) == 0) && (KPT % 4 == 0);
-    if (vec && nvalid == KPT) {
+    const bool use_hist = ghist && a.k > 0 && a.k < M;
+    uint32_t g0 = 0u, g1 = 0u;
+    if (use_hist) {
+        g0 = ghist[tid];
+        g1 = ghist[tid + kSelThreads];
+    }
+    float v[KPT];
+    const bool vec = (reinterpret_cast<uintptr_t>(s) & 15) == 0;
 #pragma unroll
-        for (int i = 0; i < KPT; i += 4) {
-            const float4 f = *reinterpret_cast<const float4*>(s + seg + i);
-            key[i] = score_key(f.x);
-            key[i + 1] = score_key(f.y);
-            key[i + 2] = score_key(f.z);
-            key[i + 3] = score_key(f.w);
+    for (int c = 0; c < CH; ++c) {
+        const int i0 = 4096 * c + 4 * tid;
+        if (vec && i0 + 3 < M) {
+            const float4 f = *reinterpret_cast<const float4*>(s + i0);
+            v[4 * c] = f.x;
+            v[4 * c + 1] = f.y;
+            v[4 * c + 2] = f.z;
+            v[4 * c + 3] = f.w;
+        } else if (i0 < M) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * c + e] = s[min(i0 + e, M - 1)];   // in bounds; past M is masked
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[4 * c + e] = 0.0f;
         }
-    } else {
+    }
+    uint32_t key[KPT];
+    uint32_t valid = 0u;   // bit j: key j lies inside the row
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) key[i] = (i < nvalid) ? score_key(s[seg + i]) : 0u;
+    for (int j = 0; j < KPT; ++j) {
+        const bool ok = 4096 * (j >> 2) + 4 * tid + (j & 3) < M;
+        key[j] = ok ? score_key(v[j]) : 0u;
+        valid |= (uint32_t)ok << j;
+    }
+    // the three digit histograms are zeroed (or, for the first, filled from the state) before the first barrier
+    sh.hist[tid] = g0;
+    sh.hist[tid + kSelThreads] = g1;
+    hist2[tid] = 0u;
+    hist2[tid + kSelThreads] = 0u;
+    hist3[tid] = 0u;
+    gtbits[tid] = 0u;
+    eqbits[tid] = 0u;
+    if (tid == 0) {   // defaults keep every later index in range even for a state that does not match the scores
+        sh.digit = 0u;
+        sh.krem = 0u;
+        sh.dcount = 0u;
     }
     if (a.k > 0) {
-        uint32_t krem = 0;
-        const uint32_t T = radix_threshold(a.k, M, [&](auto fn) {
+        // MSB-first radix select on the registers: digits of 11, 11 and 10 bits, each histogram searched by one wave
+        uint32_t T = 0u, krem = 0xffffffffu;   // k >= M: every key is selected
+        __syncthreads();
+        if (a.k < M) {
+            if (!use_hist) {
 #pragma unroll
-            for (int i = 0; i < KPT; ++i)
-                if (i < nvalid) fn(key[i]);
-        }, sh, ghist, krem);
-        init_sortbuf(a, sh);
-        uint32_t cgt = 0, ceq = 0;
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            if (i < nvalid) {
-                cgt += key[i] > T;
-                ceq += key[i] == T;
+                for (int j = 0; j < KPT; ++j)
+                    if ((valid >> j) & 1u) atomicAdd(&sh.hist[key[j] >> 21], 1u);
+                __syncthreads();
             }
+            find_digit_wave(sh, sh.hist, (uint32_t)a.k, 2048);
+            const uint32_t d1 = sh.digit & 2047u;
+            krem = sh.krem;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                if (((valid >> j) & 1u) && (key[j] >> 21) == d1) atomicAdd(&hist2[(key[j] >> 10) & 2047u], 1u);
+            __syncthreads();
+            find_digit_wave(sh, hist2, krem, 2048);
+            const uint32_t p2 = (d1 << 11) | (sh.digit & 2047u);
+            krem = sh.krem;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                if (((valid >> j) & 1u) && (key[j] >> 10) == p2) atomicAdd(&hist3[key[j] & 1023u], 1u);
+            __syncthreads();
+            find_digit_wave(sh, hist3, krem, 1024);
+            T = (p2 << 10) | (sh.digit & 1023u);
+            krem = sh.krem;
         }
+        init_sortbuf(a, sh);
+        // bitmap words: chunk c of thread t is bits 4 (t % 8) .. + 3 of word 128 c + t / 8
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            uint32_t gt = 0u, eq = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 4 * c + e;
+                const bool ok = (valid >> j) & 1u;
+                gt |= (uint32_t)(ok && key[j] > T) << e;
+                eq |= (uint32_t)(ok && key[j] == T) << e;
+            }
+            const int w = 128 * c + (tid >> 3), sh4 = 4 * (tid & 7);
+            if (gt) atomicOr(&gtbits[w], gt << sh4);
+            if (eq) atomicOr(&eqbits[w], eq << sh4);
+        }
+        __syncthreads();
+        const bool mine = tid < 128 * CH;
+        const uint32_t gw = mine ? gtbits[tid] : 0u, ew = mine ? eqbits[tid] : 0u;
         uint32_t egt, eeq;
-        block_excl_scan2(cgt, ceq, egt, eeq, sh);
-        if (cgt + ceq > 0) {
-            const Emitter em = make_emitter(a, row, sh);
+        block_excl_scan2(__popc(gw), __popc(ew), egt, eeq, sh);
+        uint32_t word = gw | ew;
+        if (word) {
             uint32_t slot = egt + min(eeq, krem);
             uint32_t ties = eeq;
-#pragma unroll
-            for (int i = 0; i < KPT; ++i) {
-                const uint32_t kk = key[i];
-                const bool eq = (i < nvalid) && kk == T;
-                const bool take = (i < nvalid) && (kk > T || (eq && ties < krem));
+            const bool direct = a.order == ATTNLAB_ORDER_POSITION && !a.top_idx && !a.top_val;
+            const int S = a.lo + (a.legal - a.hi) + a.k;
+            int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride + a.lo : nullptr;
+            int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S + a.lo : nullptr;
+            const int64_t base = (int64_t)row * a.C + a.lo;
+            const Emitter em = make_emitter(a, row, sh);
+            while (word) {
+                const uint32_t b = __ffs(word) - 1;
+                word &= word - 1;
+                const bool eq = (ew >> b) & 1u;
+                const bool take = !eq || ties < krem;
                 ties += eq;
-                if (take) em.put(slot++, seg + i, kk);
+                if (!take) continue;
+                const int idx = 32 * tid + (int)b;
+                if (direct) {
+                    // the decode step's row list: candidate m at slot lo + (its rank), as the Emitter would write it
+                    if (slot < (uint32_t)a.k) {
+                        if (rows) rows[slot] = a.lo + idx;
+                        if (flat) flat[slot] = base + idx;
+                    }
+                } else {
+                    em.put(slot, idx, score_key(s[idx]));
+                }
+                ++slot;
             }
         }
     }
@@ -443,12 +540,12 @@ __global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a) {
 }
 
 static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
-    const int kpt = (a.M + kSelThreads - 1) / kSelThreads;
+    const int chunks = (a.M + 4095) / 4096;
     const dim3 grid(R), block(kSelThreads);
-    if (kpt <= 4) hipLaunchKernelGGL(select_reg<4>, grid, block, 0, s, a);
-    else if (kpt <= 8) hipLaunchKernelGGL(select_reg<8>, grid, block, 0, s, a);
-    else if (kpt <= 16) hipLaunchKernelGGL(select_reg<16>, grid, block, 0, s, a);
-    else if (kpt <= 32) hipLaunchKernelGGL(select_reg<32>, grid, block, 0, s, a);
+    if (chunks <= 1) hipLaunchKernelGGL(select_reg<1>, grid, block, 0, s, a);
+    else if (chunks <= 2) hipLaunchKernelGGL(select_reg<2>, grid, block, 0, s, a);
+    else if (chunks <= 4) hipLaunchKernelGGL(select_reg<4>, grid, block, 0, s, a);
+    else if (chunks <= kRegMaxChunks) hipLaunchKernelGGL(select_reg<kRegMaxChunks>, grid, block, 0, s, a);
     else hipLaunchKernelGGL(select_stream, grid, block, 0, s, a);
     return check_launch("select");
 }
