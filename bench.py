@@ -82,6 +82,16 @@ def parse_args():
     ap.add_argument("--c5-context", type=int, default=32768)
     ap.add_argument("--c5-batch", type=int, default=16)
     ap.add_argument("--c5-chunk", type=int, default=2048, help="prefill chunk of the configs[4] run")
+    ap.add_argument("--p0", action="store_true",
+                    help="instead of the bench line: the reference's P0 score bench (bench/p0_score_kernel.py) on the "
+                         "HIP score ops: batch 1, G=8, h=2, 28 rotating layers per length; PyTorch chain / score-only "
+                         "vs fused one- and two-launch; numerics and the stop gate; one JSON line per length + summary")
+    ap.add_argument("--p1", action="store_true",
+                    help="instead of the bench line: the reference's P1 attend bench (bench/p1_attend_kernel.py) on "
+                         "the HIP attend: index_select + subset attention vs the gather-free attend at P = 1, 2, 4, 8; "
+                         "numerics and the stop gate; one JSON line per length + summary")
+    ap.add_argument("--p-lengths", type=int, nargs="+", default=[8192, 16384, 32256], help="N0 of --p0 / --p1")
+    ap.add_argument("--p-layers", type=int, default=28, help="rotating layers of --p0 / --p1")
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
@@ -732,6 +742,178 @@ def run_c5(torch, dev, args):
     return 0
 
 
+def p_geometry(N0, rho):
+    """Legal length N0 + 1, capacity N0 + 128, the selection layout and k of the reference's P0/P1 benches."""
+    from attention_lab.selection import fixed_budget, selection_layout
+    L, C = N0 + 1, N0 + 128
+    lay = selection_layout(L)
+    k = lay.clamp_k(fixed_budget(L, rho))
+    return L, C, lay, k
+
+
+def run_p0(torch, dev, args):
+    """bench/p0_score_kernel.py on this build: the D chain's scoring segment (z column of the newest key, u, the scores
+    of every candidate) per layer, batch 1. Strategies: pytorch_chain (project_keys + column copy + project_queries +
+    candidate_scores, bf16 matmuls on the GPU), pytorch_score_only (candidate_scores from a precomputed u),
+    fused_1launch (HipScore.fused) and fused_2launch (HipScore.two_launch). Each is a graph over `layers` index tables
+    timed with HIP events. Numerics on layer 0: fused fp32 scores against an fp32 matmul of the same bf16 values, the
+    z column against the RNE of its fp32 value, top-k set agreement with the chain's bf16 scores. The stop gate is the
+    reference's (p0_score_kernel.py:33)."""
+    from attention_lab.hip_score import HipScore
+    from attention_lab.indexer import GroupedIndexer
+    gate = {"fused_us_max_32k": 80.0, "ratio_vs_chain_max": 0.75, "scores_atol": 1e-5, "scores_rel_norm": 1e-5,
+            "z_rel_ulp": 2.0 ** -8}
+    hs, bf = HipScore(), torch.bfloat16
+    G, h, d, r, nl = 8, 2, 128, 32, args.p_layers
+    blocks = []
+    for N0 in args.p_lengths:
+        L, C, lay, k = p_geometry(N0, args.rho)
+        lo, hi, wc, M = lay.candidate_lo, lay.candidate_hi, L - 1, lay.candidate_count
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(args.seed + N0)
+        zT = [torch.randn(G, r, C, generator=gen, device=dev).to(bf) for _ in range(nl)]
+        k_new = torch.randn(G, d, generator=gen, device=dev).to(bf)
+        q_cat = torch.randn(G, h * d, generator=gen, device=dev).to(bf)
+        idx = GroupedIndexer(G, h, d, r, device=dev, dtype=bf, seed=args.seed)
+        wk, wq_t = idx.wk, idx.wq_t_scaled
+        outs = [torch.empty(G, M, dtype=torch.float32, device=dev) for _ in range(nl)]
+        ubufs = [torch.empty(G, r, dtype=torch.float32, device=dev) for _ in range(nl)]
+        u_pre = torch.matmul(q_cat.unsqueeze(1), wq_t)                       # [G, 1, r]
+        kcol = k_new.unsqueeze(-1).contiguous()                               # [G, d, 1]
+
+        def chain(i):
+            zT[i][:, :, wc:wc + 1].copy_(torch.matmul(wk, kcol))
+            u = torch.matmul(q_cat.unsqueeze(1), wq_t)
+            return torch.matmul(u, zT[i][:, :, lo:hi])
+
+        strategies = {
+            "pytorch_chain": chain,
+            "pytorch_score_only": lambda i: torch.matmul(u_pre, zT[i][:, :, lo:hi]),
+            "fused_1launch": lambda i: hs.fused(zT[i], k_new, wk, q_cat, wq_t, lo, hi, wc, out=outs[i]),
+            "fused_2launch": lambda i: hs.two_launch(zT[i], k_new, wk, q_cat, wq_t, lo, hi, wc, out=outs[i],
+                                                     u_buf=ubufs[i]),
+        }
+        us = {name: time_rotating(torch, fn, nl) for name, fn in strategies.items()}
+        # numerics on layer 0
+        z0 = zT[0].clone()
+        fused = hs.fused(z0, k_new, wk, q_cat, wq_t, lo, hi, wc)
+        u32 = torch.matmul(q_cat.float().unsqueeze(1), wq_t.float())
+        ref = torch.matmul(u32, zT[0].float()[:, :, lo:hi]).squeeze(1)
+        diff = (fused - ref).abs()
+        atol, rel = float(diff.max()), float(diff.norm() / ref.norm())
+        zref = torch.matmul(wk.float(), k_new.float().unsqueeze(-1)).squeeze(-1)
+        zgot = z0[:, :, wc].float()
+        z_rel = float(((zgot - zref).abs() / zref.abs().clamp_min(1e-30)).max())
+        z_bits = float((z0[:, :, wc] == zref.to(bf)).float().mean())
+        chain_scores = chain(0).squeeze(1).float()
+        kk = max(1, k)
+        a_idx = torch.topk(fused, kk, dim=-1).indices
+        b_idx = torch.topk(chain_scores, kk, dim=-1).indices
+        agree = float(sum(len(set(a.tolist()) & set(b.tolist())) for a, b in zip(a_idx, b_idx)) / (G * kk))
+        torch.cuda.synchronize()
+        num = {"scores_max_abs": atol, "scores_rel_norm": rel, "z_max_rel": z_rel, "z_bitwise_rne": z_bits,
+               "topk_agreement_vs_chain_bf16": agree,
+               "pass": atol <= gate["scores_atol"] and rel <= gate["scores_rel_norm"] and z_rel <= gate["z_rel_ulp"]}
+        block = {"bench": "p0", "N0": N0, "legal": L, "capacity": C, "candidates": M, "k": k, "layers": nl,
+                 "us_per_layer": {n: round(v, 2) for n, v in us.items()}, "numerics": num}
+        print(json.dumps(block), flush=True)
+        blocks.append(block)
+        del zT, outs
+        torch.cuda.empty_cache()
+    big = [b for b in blocks if b["N0"] >= 32000]
+    g = {"gate": gate, "numerics_pass_all": all(b["numerics"]["pass"] for b in blocks)}
+    if big:
+        b = big[-1]
+        fused_us = min(b["us_per_layer"]["fused_1launch"], b["us_per_layer"]["fused_2launch"])
+        g.update({"evaluated_at_N0": b["N0"], "fused_us": fused_us,
+                  "ratio_vs_chain": round(fused_us / b["us_per_layer"]["pytorch_chain"], 4)})
+        g["pass"] = (g["numerics_pass_all"] and fused_us <= gate["fused_us_max_32k"]
+                     and g["ratio_vs_chain"] <= gate["ratio_vs_chain_max"])
+    print(json.dumps({"bench": "p0", "summary": g}), flush=True)
+    return 0
+
+
+def run_p1(torch, dev, args):
+    """bench/p1_attend_kernel.py on this build: the read of the S selected K and V rows and the attention over them,
+    batch 1, G=8, h=2. Rows are F and k random distinct candidates per layer and group (cat order), prepared outside
+    the timed region. Strategies: pytorch_gather (flat index_select of K and of V, then subset attention as bf16
+    matmuls with the transposed K made contiguous, softmax in fp32), fused_attend_P{1,2,4,8} (HipAttend, bf16 output)
+    and, as context only, the dense kernel over the legal length. Graphs over `layers` caches, HIP events. Numerics on
+    layer 0: the fp32 kernel output against an fp32 masked softmax over the same rows, the bf16 output against the
+    RNE of the fp32 output. The stop gate is the reference's (p1_attend_kernel.py:32)."""
+    from attention_lab import hip_attend
+    gate = {"fused_us_max_at_S1076": 60.0, "ratio_vs_gather_sdpa_max": 0.80, "out_atol": 5e-5, "out_rel_norm": 1e-5,
+            "bf16_ulp": 2.0 ** -8}
+    ha, bf = hip_attend.HipAttend(), torch.bfloat16
+    G, h, d, nl = 8, 2, 128, args.p_layers
+    scale = 1.0 / math.sqrt(d)
+    blocks = []
+    for N0 in args.p_lengths:
+        L, C, lay, k = p_geometry(N0, args.rho)
+        S = lay.fixed_count + k
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(args.seed + N0)
+        K = [torch.randn(G, C, d, generator=gen, device=dev).to(bf) for _ in range(nl)]
+        V = [torch.randn(G, C, d, generator=gen, device=dev).to(bf) for _ in range(nl)]
+        q = torch.randn(G, h, d, generator=gen, device=dev).to(bf)
+        fixed = torch.tensor(lay.fixed_positions(), device=dev, dtype=torch.long)
+        rows, flats = [], []
+        for _ in range(nl):
+            pick = torch.stack([torch.randperm(lay.candidate_count, generator=gen, device=dev)[:k] for _ in range(G)])
+            r32 = torch.cat([fixed.expand(G, -1), pick + lay.candidate_lo], dim=1).to(torch.int32).contiguous()
+            rows.append(r32)
+            flats.append((r32.long() + torch.arange(G, device=dev).view(G, 1) * C).reshape(-1))
+        outb = torch.empty(G, h, d, dtype=bf, device=dev)
+        part = torch.empty(G * 8 * h * (d + 2), dtype=torch.float32, device=dev)
+
+        def gather(i):
+            ks = K[i].reshape(G * C, d).index_select(0, flats[i]).view(G, S, d)
+            vs = V[i].reshape(G * C, d).index_select(0, flats[i]).view(G, S, d)
+            sc = torch.matmul(q, ks.transpose(1, 2).contiguous()).float() * scale
+            return torch.matmul(torch.softmax(sc, -1).to(bf), vs)
+
+        strategies = {"pytorch_gather": gather}
+        for P in (1, 2, 4, 8):
+            strategies[f"fused_attend_P{P}"] = (lambda P: lambda i: ha(K[i], V[i], q, rows[i], partitions=P,
+                                                                       out_dtype=bf, out=outb, part=part))(P)
+        strategies["dense_full_context"] = lambda i: hip_attend.dense_decode(q.unsqueeze(0), K[i].unsqueeze(0),
+                                                                             V[i].unsqueeze(0), L)
+        us = {name: time_rotating(torch, fn, nl) for name, fn in strategies.items()}
+        # numerics on layer 0
+        o32 = ha(K[0], V[0], q, rows[0], partitions=4, out_dtype=torch.float32)
+        o16 = ha(K[0], V[0], q, rows[0], partitions=4, out_dtype=bf)
+        kf, vf = K[0].float(), V[0].float()
+        s = torch.matmul(q.float(), kf.transpose(1, 2).contiguous()) * scale        # [G, h, C] fp32
+        mask = torch.full((G, 1, C), float("-inf"), device=dev)
+        mask.scatter_(2, rows[0].long().unsqueeze(1), 0.0)
+        ref = torch.matmul(torch.softmax(s + mask, -1), vf)
+        diff = (o32 - ref).abs()
+        atol, rel = float(diff.max()), float(diff.norm() / ref.norm())
+        bits = float((o16 == o32.to(bf)).float().mean())
+        ulp = float(((o16.float() - o32).abs() / o32.abs().clamp_min(1e-30)).max())
+        torch.cuda.synchronize()
+        num = {"out_max_abs": atol, "out_rel_norm": rel, "bf16_equal_rne": bits, "bf16_max_rel": ulp,
+               "pass": atol <= gate["out_atol"] and rel <= gate["out_rel_norm"] and ulp <= gate["bf16_ulp"]}
+        block = {"bench": "p1", "N0": N0, "legal": L, "capacity": C, "k": k, "S": S, "layers": nl,
+                 "us_per_layer": {n: round(v, 2) for n, v in us.items()}, "numerics": num}
+        print(json.dumps(block), flush=True)
+        blocks.append(block)
+        del K, V
+        torch.cuda.empty_cache()
+    big = [b for b in blocks if b["N0"] >= 32000]
+    g = {"gate": gate, "numerics_pass_all": all(b["numerics"]["pass"] for b in blocks)}
+    if big:
+        b = big[-1]
+        fused = {n: v for n, v in b["us_per_layer"].items() if n.startswith("fused")}
+        best = min(fused, key=fused.get)
+        g.update({"evaluated_at_S": b["S"], "best": best, "fused_us": fused[best],
+                  "ratio_vs_gather": round(fused[best] / b["us_per_layer"]["pytorch_gather"], 4)})
+        g["pass"] = (g["numerics_pass_all"] and fused[best] <= gate["fused_us_max_at_S1076"]
+                     and g["ratio_vs_gather"] <= gate["ratio_vs_gather_sdpa_max"])
+    print(json.dumps({"bench": "p1", "summary": g}), flush=True)
+    return 0
+
+
 def run_c4(torch, dev, args):
     """configs[3] through the wrapper on the HIP kernels: greedy decode on the full read (A); the same tokens on the
     sparse read (D0, rho = 1/32) and on the sparse read with k0 = capacity (every candidate selected, which must
@@ -937,6 +1119,10 @@ def main() -> int:
         return run_c4(torch, dev, args)
     if args.c5:
         return run_c5(torch, dev, args)
+    if args.p0:
+        return run_p0(torch, dev, args)
+    if args.p1:
+        return run_p1(torch, dev, args)
 
     t_setup = time.perf_counter()
     ls = LayerStack(torch, dev, batch=args.batch, groups=args.groups, hpg=args.heads_per_group, context=args.context,

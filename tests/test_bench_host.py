@@ -99,3 +99,14 @@ def test_mfma_busy_fraction(tmp_path, capsys):
 def test_committed_profiles_feed_the_bench_line():
     assert bench.measured_traffic() == pytest.approx(288_780_776, rel=1e-3)
     assert 0.0 < bench.mfma_busy_from_profile() < 1.0
+
+
+def test_p0_p1_geometry_matches_the_reference_benches():
+    """Legal length N0 + 1, capacity N0 + 128, k from the rho rule: the P1 gate's S = 1076 sits at N0 = 32256
+    (p1_attend_kernel.py:32 names S1076; the lengths are p0_score_kernel.py:36's)."""
+    L, C, lay, k = bench.p_geometry(32256, 1 / 32)
+    assert (L, C) == (32257, 32384)
+    assert (lay.candidate_lo, lay.candidate_hi, lay.candidate_count) == (4, 32193, 32189)
+    assert lay.fixed_count + k == 1076 and k == 1008
+    L, C, lay, k = bench.p_geometry(8192, 1 / 32)
+    assert lay.fixed_count + k == 324 and k == 256
