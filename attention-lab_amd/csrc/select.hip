@@ -81,30 +81,11 @@ __device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_
     block_scan2<kSelThreads>(a, b, ea, eb, ta, tb, sh.wave_tot);
 }
 
-// With the histogram of one digit complete in hist[0..nbins) (LDS), find the digit D holding the krem-th largest key:
-// count(digit > D) < krem <= count(digit >= D). Thread t owns bins [2t, 2t+1]; the counts above a thread come from
-// an exclusive scan over the threads in reverse order. Publishes D and the new krem; ends synchronised.
-__device__ __forceinline__ void find_digit(SelectShared& sh, const uint32_t* hist, uint32_t krem, int nbins) {
-    const int tid = threadIdx.x;
-    const int rt = kSelThreads - 1 - tid;       // reverse rank: thread 1023 owns the lowest bins
-    const int b0 = 2 * rt;
-    const uint32_t c0 = b0 < nbins ? hist[b0] : 0u, c1 = b0 + 1 < nbins ? hist[b0 + 1] : 0u;
-    uint32_t above, unused;
-    block_excl_scan2(c0 + c1, 0u, above, unused, sh);   // keys in bins owned by lower tids = higher bins
-    if (above < krem && above + c1 >= krem) {
-        sh.digit = (uint32_t)(b0 + 1);
-        sh.krem = krem - above;
-    } else if (above + c1 < krem && above + c1 + c0 >= krem) {
-        sh.digit = (uint32_t)b0;
-        sh.krem = krem - above - c1;
-    }
-    __syncthreads();
-}
-
-// find_digit done by wave 0 alone, for nbins = 1024 or 2048: lane l sums the l-th chunk of nbins / 64 bins from the
+// The digit D holding the krem-th largest key of a complete histogram (count(digit > D) < krem <= count(digit >= D)),
+// found by wave 0 alone, for nbins = 1024 or 2048: lane l sums the l-th chunk of nbins / 64 bins from the
 // top (starting at a lane-dependent 16-byte segment, so the lanes spread over the LDS banks), a DPP scan over the
 // lanes finds the chunk holding the krem-th largest key, and a second scan over that chunk's bins, one per lane, finds
-// the bin. Publishes D, the new krem and the count of bin D; one barrier instead of the block scan's three.
+// the bin. Publishes D, the new krem and the count of bin D; ends with one barrier.
 __device__ __forceinline__ void find_digit_wave(SelectShared& sh, const uint32_t* hist, uint32_t krem, int nbins) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
@@ -133,43 +114,6 @@ __device__ __forceinline__ void find_digit_wave(SelectShared& sh, const uint32_t
         }
     }
     __syncthreads();
-}
-
-// Threshold search. `for_each_key(fn)` calls fn(key) for every valid key of this thread. Returns T; sets krem_out to
-// the number of keys equal to T that are selected. `ghist` (nullable) is the first digit's histogram of this row.
-template <typename ForEach>
-__device__ __forceinline__ uint32_t radix_threshold(int k, int M, ForEach for_each_key, SelectShared& sh,
-                                                    const uint32_t* ghist, uint32_t& krem_out) {
-    const int tid = threadIdx.x;
-    if (k >= M) {  // every key is selected: threshold below every key, all ties taken
-        krem_out = 0xffffffffu;
-        return 0u;
-    }
-    constexpr int kShift[3] = {21, 10, 0};
-    constexpr int kBins[3] = {2048, 2048, 1024};
-    uint32_t prefix = 0, pmask = 0, krem = (uint32_t)k;
-#pragma unroll
-    for (int pass = 0; pass < 3; ++pass) {
-        const int shift = kShift[pass], nb = kBins[pass];
-        const uint32_t dmask = (uint32_t)nb - 1u;
-        if (pass == 0 && ghist) {
-            for (int i = tid; i < nb; i += kSelThreads) sh.hist[i] = ghist[i];
-            __syncthreads();
-        } else {
-            for (int i = tid; i < nb; i += kSelThreads) sh.hist[i] = 0u;
-            __syncthreads();
-            for_each_key([&](uint32_t key) {
-                if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
-            });
-            __syncthreads();
-        }
-        find_digit(sh, sh.hist, krem, nb);
-        prefix |= sh.digit << shift;
-        pmask |= dmask << shift;
-        krem = sh.krem;
-    }
-    krem_out = krem;
-    return prefix;
 }
 
 // Length of the score-order sort: k rounded up to a power of two, at least one 128-element chunk.
@@ -492,43 +436,165 @@ __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
     finish_row(a, row, sh);
 }
 
-// One row with 1024 threads, keys re-read from global memory in every pass (any M). Used for long rows and as the
-// fallback of the tiled select.
-__device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared& sh) {
+// One row of any length with 1024 threads (rows past 32768 keys without a select state, and the resolve whose
+// threshold bin overflowed its candidate list). The row is re-read from global memory (L2-resident after the first
+// pass) in every pass, coalesced as in select_reg: thread t reads keys 4096 c + 4 t + e, four chunks' loads in flight
+// at a time. Threshold: the first digit's histogram (from the state, or built by a pass), then two passes over the keys
+// that share the prefix, each histogram searched by one wave. Emission in windows of 32768 keys through select_reg's
+// two LDS bitmaps, one block scan per window, with the counts of the earlier windows carried over.
+struct StreamLds {
+    uint32_t* hist2;    // 2048 words
+    uint32_t* hist3;    // 1024
+    uint32_t* gtbits;   // kRegWords
+    uint32_t* eqbits;   // kRegWords
+};
+
+// fn(c, key[4], valid mask) for every chunk c of 4096 keys this thread touches (keys 4096 c + 4 t + e).
+template <typename Fn>
+__device__ __forceinline__ void for_each_chunk(const float* s, int M, int c_begin, int c_end, Fn fn) {
+    constexpr int kBatch = 4;
     const int tid = threadIdx.x;
-    const int seglen = (a.M + kSelThreads - 1) / kSelThreads;
-    const float* s = a.scores + (size_t)row * a.score_stride;
-    const int seg = tid * seglen;
-    const int nvalid = max(0, min(seglen, a.M - seg));
-    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kSelectStateWords : nullptr;
-    if (a.k > 0) {
-        uint32_t krem = 0;
-        const uint32_t T = radix_threshold(a.k, a.M, [&](auto fn) {
-            for (int i = 0; i < nvalid; ++i) fn(score_key(s[seg + i]));
-        }, sh, ghist, krem);
-        init_sortbuf(a, sh);
-        uint32_t cgt = 0, ceq = 0;
-        for (int i = 0; i < nvalid; ++i) {
-            const uint32_t kk = score_key(s[seg + i]);
-            cgt += kk > T;
-            ceq += kk == T;
-        }
-        uint32_t egt, eeq;
-        block_excl_scan2(cgt, ceq, egt, eeq, sh);
-        if (cgt + ceq > 0) {
-            const Emitter em = make_emitter(a, row, sh);
-            uint32_t slot = egt + min(eeq, krem);
-            uint32_t ties = eeq;
-            for (int i = 0; i < nvalid; ++i) {
-                const uint32_t kk = score_key(s[seg + i]);
-                const bool eq = kk == T;
-                const bool take = kk > T || (eq && ties < krem);
-                ties += eq;
-                if (take) em.put(slot++, seg + i, kk);
+    const bool vec = (reinterpret_cast<uintptr_t>(s) & 15) == 0;
+    for (int c0 = c_begin; c0 < c_end; c0 += kBatch) {
+        float v[4 * kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int i0 = 4096 * (c0 + u) + 4 * tid;
+            if (c0 + u < c_end && vec && i0 + 3 < M) {
+                const float4 f = *reinterpret_cast<const float4*>(s + i0);
+                v[4 * u] = f.x;
+                v[4 * u + 1] = f.y;
+                v[4 * u + 2] = f.z;
+                v[4 * u + 3] = f.w;
+            } else if (c0 + u < c_end && i0 < M) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * u + e] = s[min(i0 + e, M - 1)];   // in bounds; past M is masked
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * u + e] = 0.0f;
             }
         }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (c0 + u >= c_end) break;
+            const int i0 = 4096 * (c0 + u) + 4 * tid;
+            uint32_t key[4], valid = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool ok = i0 + e < M;
+                key[e] = ok ? score_key(v[4 * u + e]) : 0u;
+                valid |= (uint32_t)ok << e;
+            }
+            fn(c0 + u, key, valid);
+        }
     }
-    if (ghist)
+}
+
+__device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared& sh, const StreamLds& L) {
+    const int tid = threadIdx.x;
+    const int M = a.M;
+    const int nch = (M + 4095) / 4096;
+    const float* s = a.scores + (size_t)row * a.score_stride;
+    uint32_t* ghist = a.hist ? a.hist + (size_t)row * kSelectStateWords : nullptr;
+    const bool use_hist = ghist && a.k > 0 && a.k < M;
+    for (int i = tid; i < kHistBins; i += kSelThreads) sh.hist[i] = use_hist ? ghist[i] : 0u;
+    for (int i = tid; i < 2048; i += kSelThreads) L.hist2[i] = 0u;
+    for (int i = tid; i < 1024; i += kSelThreads) L.hist3[i] = 0u;
+    if (tid == 0) {   // defaults keep every later index in range even for a state that does not match the scores
+        sh.digit = 0u;
+        sh.krem = 0u;
+        sh.dcount = 0u;
+    }
+    __syncthreads();
+    if (a.k > 0) {
+        uint32_t T = 0u, krem = 0xffffffffu;   // k >= M: every key is selected
+        if (a.k < M) {
+            if (!use_hist) {
+                for_each_chunk(s, M, 0, nch, [&](int, const uint32_t* key, uint32_t valid) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if ((valid >> e) & 1u) atomicAdd(&sh.hist[key[e] >> 21], 1u);
+                });
+                __syncthreads();
+            }
+            find_digit_wave(sh, sh.hist, (uint32_t)a.k, 2048);
+            const uint32_t d1 = sh.digit & 2047u;
+            krem = sh.krem;
+            for_each_chunk(s, M, 0, nch, [&](int, const uint32_t* key, uint32_t valid) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (((valid >> e) & 1u) && (key[e] >> 21) == d1) atomicAdd(&L.hist2[(key[e] >> 10) & 2047u], 1u);
+            });
+            __syncthreads();
+            find_digit_wave(sh, L.hist2, krem, 2048);
+            const uint32_t p2 = (d1 << 11) | (sh.digit & 2047u);
+            krem = sh.krem;
+            for_each_chunk(s, M, 0, nch, [&](int, const uint32_t* key, uint32_t valid) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (((valid >> e) & 1u) && (key[e] >> 10) == p2) atomicAdd(&L.hist3[key[e] & 1023u], 1u);
+            });
+            __syncthreads();
+            find_digit_wave(sh, L.hist3, krem, 1024);
+            T = (p2 << 10) | (sh.digit & 1023u);
+            krem = sh.krem;
+        }
+        init_sortbuf(a, sh);
+        const bool direct = a.order == ATTNLAB_ORDER_POSITION && !a.top_idx && !a.top_val;
+        const int S = a.lo + (a.legal - a.hi) + a.k;
+        int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride + a.lo : nullptr;
+        int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S + a.lo : nullptr;
+        const int64_t base = (int64_t)row * a.C + a.lo;
+        const Emitter em = make_emitter(a, row, sh);
+        uint32_t gt_before = 0u, eq_before = 0u;   // selected-above and tied keys of the earlier windows
+        for (int c_w = 0; c_w < nch; c_w += kRegMaxChunks) {
+            L.gtbits[tid] = 0u;
+            L.eqbits[tid] = 0u;
+            __syncthreads();
+            for_each_chunk(s, M, c_w, min(nch, c_w + kRegMaxChunks), [&](int c, const uint32_t* key, uint32_t valid) {
+                uint32_t gt = 0u, eq = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = (valid >> e) & 1u;
+                    gt |= (uint32_t)(ok && key[e] > T) << e;
+                    eq |= (uint32_t)(ok && key[e] == T) << e;
+                }
+                const int w = 128 * (c - c_w) + (tid >> 3), sh4 = 4 * (tid & 7);
+                if (gt) atomicOr(&L.gtbits[w], gt << sh4);
+                if (eq) atomicOr(&L.eqbits[w], eq << sh4);
+            });
+            __syncthreads();
+            const uint32_t gw = L.gtbits[tid], ew = L.eqbits[tid];
+            uint32_t egt, eeq, tgt, teq;
+            block_scan2<kSelThreads>(__popc(gw), __popc(ew), egt, eeq, tgt, teq, sh.wave_tot);
+            uint32_t word = gw | ew;
+            if (word) {
+                uint32_t ties = eq_before + eeq;
+                uint32_t slot = gt_before + egt + min(ties, krem);
+                while (word) {
+                    const uint32_t b = __ffs(word) - 1;
+                    word &= word - 1;
+                    const bool eq = (ew >> b) & 1u;
+                    const bool take = !eq || ties < krem;
+                    ties += eq;
+                    if (!take) continue;
+                    const int idx = 4096 * c_w + 32 * tid + (int)b;
+                    if (direct) {
+                        if (slot < (uint32_t)a.k) {
+                            if (rows) rows[slot] = a.lo + idx;
+                            if (flat) flat[slot] = base + idx;
+                        }
+                    } else {
+                        em.put(slot, idx, score_key(s[idx]));
+                    }
+                    ++slot;
+                }
+            }
+            gt_before += tgt;
+            eq_before += teq;
+        }
+    }
+    if (ghist)  // leave the first-digit histogram zeroed for the next score/select pair
         for (int i = tid; i < kSelectStateWords; i += kSelThreads) ghist[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);
@@ -536,7 +602,11 @@ __device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared&
 
 __global__ __launch_bounds__(kSelThreads) void select_stream(SelectArgs a) {
     __shared__ SelectShared sh;
-    select_row_streaming(a, xcd_contiguous_block(), sh);
+    __shared__ __attribute__((aligned(16))) uint32_t hist2[2048];
+    __shared__ __attribute__((aligned(16))) uint32_t hist3[1024];
+    __shared__ uint32_t gtbits[kRegWords];
+    __shared__ uint32_t eqbits[kRegWords];
+    select_row_streaming(a, xcd_contiguous_block(), sh, StreamLds{hist2, hist3, gtbits, eqbits});
 }
 
 static int launch_select(const SelectArgs& a, int R, hipStream_t s) {
@@ -675,7 +745,7 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     constexpr int kCandPerThread = CAP / kSelThreads;
     __shared__ SelectShared sh;                 // sortbuf holds the candidate list (as uint32 indices)
     __shared__ __attribute__((aligned(16))) uint32_t hist3[1024];
-    __shared__ uint32_t bits[kMaxWords];
+    __shared__ __attribute__((aligned(16))) uint32_t bits[kMaxWords];
     const int row = xcd_contiguous_block();   // the XCD that classified the row
     const int tid = threadIdx.x;
     const int W = t.W;
@@ -705,7 +775,8 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     uint32_t ec, unused, n, n_above;
     block_scan2<kSelThreads>(nc, na, ec, unused, n, n_above, sh.wave_tot);
     if (n > (uint32_t)CAP) {   // too many keys share the threshold's first digit: single-workgroup select
-        select_row_streaming(a, row, sh);
+        // bits[] (the above bitmap) is no longer needed: it holds the streaming select's LDS histograms and bitmaps
+        select_row_streaming(a, row, sh, StreamLds{bits, bits + 2048, bits + 3072, bits + 3072 + kRegWords});
         return;
     }
     // candidate list in index order
