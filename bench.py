@@ -90,6 +90,10 @@ def parse_args():
                     help="instead of the bench line: the reference's P1 attend bench (bench/p1_attend_kernel.py) on "
                          "the HIP attend: index_select + subset attention vs the gather-free attend at P = 1, 2, 4, 8; "
                          "numerics and the stop gate; one JSON line per length + summary")
+    ap.add_argument("--f32-workload", action="store_true",
+                    help="instead of the bench line: the fused step over float32 index tables (a trained bank's "
+                         "dtype) at the bench shape, 8 rotating layers, graph-timed, with the bf16 step beside it; "
+                         "one JSON line (also the command profiled for the fp32 kernels)")
     ap.add_argument("--p-lengths", type=int, nargs="+", default=[8192, 16384, 32256], help="N0 of --p0 / --p1")
     ap.add_argument("--p-layers", type=int, default=28, help="rotating layers of --p0 / --p1")
     ap.add_argument("--prefill-workload", action="store_true",
@@ -742,6 +746,51 @@ def run_c5(torch, dev, args):
     return 0
 
 
+def run_f32_workload(torch, dev, args, layers=8):
+    """attnlab_sparse_decode_step_f32 (float32 zT / wq_t / wk / index query and key, bf16 K/V) and the bf16 step on the
+    same shape: B x G x L of the bench line, k from rho, position order, graphs of `layers` rotating layers. Reports
+    us per layer and the fp32 scan's table bytes (r * 4 per candidate column)."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_attend
+    from attention_lab.indexer import GroupedIndexer
+    from attention_lab.selection import fixed_budget, selection_layout
+    B, G, h, d, r, L = args.batch, args.groups, args.heads_per_group, 128, args.index_dim, args.context
+    lay = selection_layout(L)
+    lo, hi, k = lay.candidate_lo, lay.candidate_hi, lay.clamp_k(fixed_budget(L, args.rho))
+    S, C, M = lay.fixed_count + k, L, lay.candidate_count
+    lib = nat.lib()
+    P = hip_attend.sparse_partitions(B * G, S, h)
+    ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, lo, hi, L, k, P)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    K = [torch.randn(B, G, C, d, generator=gen, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    V = [torch.randn(B, G, C, d, generator=gen, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    q = torch.randn(B, G, h, d, generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty(B, G, h, d, dtype=torch.bfloat16, device=dev)
+    res = {"f32_workload": f"sparse step B={B} G={G} h={h} L={L} r={r} k={k} S={S} P={P}, {layers} rotating layers"}
+    for dt, entry in ((torch.float32, "attnlab_sparse_decode_step_f32"), (torch.bfloat16, "attnlab_sparse_decode_step")):
+        zT = [torch.randn(B, G, r, C, generator=gen, device=dev).to(dt) for _ in range(layers)]
+        idx = GroupedIndexer(G, h, d, r, device=dev, dtype=dt, seed=args.seed)
+        q_cat = torch.randn(B, G, h * d, generator=gen, device=dev).to(dt)
+        k_new = torch.randn(B, G, d, generator=gen, device=dev).to(dt)
+
+        def step(l):
+            nat.call(entry, q.data_ptr(), q_cat.data_ptr(), K[l].data_ptr(), V[l].data_ptr(), zT[l].data_ptr(),
+                     idx.wq_t_scaled.data_ptr(), idx.wk.data_ptr(), k_new.data_ptr(), B, G, h, r, C, lo, hi, L, k,
+                     L - 1, 1.0 / math.sqrt(d), nat.ORDER_POSITION, P, state.data_ptr(), ws.data_ptr(), ws_bytes,
+                     None, None, out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+
+        name = "float32" if dt == torch.float32 else "bfloat16"
+        res[f"{name}_us_per_layer"] = round(time_rotating(torch, step, layers, reps=20), 2)
+        res[f"{name}_table_bytes_per_layer"] = B * G * r * M * zT[0].element_size()
+        del zT
+        torch.cuda.empty_cache()
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def p_geometry(N0, rho):
     """Legal length N0 + 1, capacity N0 + 128, the selection layout and k of the reference's P0/P1 benches."""
     from attention_lab.selection import fixed_budget, selection_layout
@@ -1119,6 +1168,8 @@ def main() -> int:
         return run_c4(torch, dev, args)
     if args.c5:
         return run_c5(torch, dev, args)
+    if args.f32_workload:
+        return run_f32_workload(torch, dev, args)
     if args.p0:
         return run_p0(torch, dev, args)
     if args.p1:
