@@ -15,12 +15,13 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
 SELECT_STATE_WORDS = 2112
 
 ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2
+LDS_SORT_K = 8192   # ATTNLAB_LDS_SORT_K: score order past this k goes through the select scratch
 ORDER_POSITION, ORDER_SCORE = 0, 1
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 
@@ -41,7 +42,7 @@ SIGNATURES = {
     "attnlab_topk": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p]),
     "attnlab_topk_tiled": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p, _p, _i64, _p]),
     "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
-    "attnlab_select_scratch_bytes": (_i64, [_i, _i]),
+    "attnlab_select_scratch_bytes": (_i64, [_i] * 4),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_prefill_attend": (_i, [_p, _p, _p, _i64, _i, _p] + [_i] * 8 + [_f, _p]),

@@ -74,6 +74,36 @@ class DecodeRequest:
                                   self.layout.candidate_hi, self.k)
 
 
+F_TAG = "_attnlab_standard_f"   # attribute set on fixed_rows / off_lo tensors built by the selection rule here
+
+
+def tag_standard_f(fixed_rows: torch.Tensor, off_lo: torch.Tensor, lo: int, hi: int, legal: int, capacity: int):
+    """Mark (fixed_rows, off_lo) as the rule's F of (lo, hi, legal) in a cache of `capacity` rows per (b, g), so the
+    HIP steps accept them without comparing their values on the device."""
+    key = (int(lo), int(hi), int(legal), int(capacity))
+    setattr(fixed_rows, F_TAG, key)
+    setattr(off_lo, F_TAG, key)
+    return fixed_rows, off_lo
+
+
+def check_standard_f(fixed_rows, off_lo, lo: int, hi: int, legal: int, capacity: int) -> None:
+    """The HIP step writes F itself from (lo, hi, legal) (its row list is F = [0, lo) U [hi, legal) then the top-k),
+    where the reference concatenates the fixed_rows it is given (decode.py:86-93). Every caller of the reference passes
+    the rule's F (decode.py:179-194, qwen_wrap.py:169-181); anything else is refused rather than silently replaced.
+    Tensors tagged by tag_standard_f pass without a device read; others are compared on the device (one sync)."""
+    key = (int(lo), int(hi), int(legal), int(capacity))
+    if getattr(fixed_rows, F_TAG, None) == key and getattr(off_lo, F_TAG, None) == key:
+        return
+    B, G = int(fixed_rows.shape[0]), int(fixed_rows.shape[1])
+    offsets = row_offsets(B, G, capacity, fixed_rows.device)
+    pos = torch.tensor(list(range(lo)) + list(range(hi, legal)), dtype=torch.long, device=fixed_rows.device)
+    want = pos.view(1, 1, -1) + offsets
+    if (tuple(fixed_rows.shape) != tuple(want.shape) or not torch.equal(fixed_rows.long(), want)
+            or not torch.equal(off_lo.long(), offsets + lo)):
+        raise ValueError("fixed_rows / off_lo must hold the selection rule's F = [0, lo) U [hi, legal) plus the row "
+                         "offsets (b*G + g)*C: the HIP step writes F from (lo, hi, legal) and cannot read another set")
+
+
 def prepare_request(batch: int, groups: int, capacity: int, *, valid_length: int, query_position: int, rho: float,
                     device, n0=None, fixed_prefix: int = FIXED_PREFIX, fixed_recent: int = FIXED_RECENT) -> DecodeRequest:
     """Fix k0 from the request's starting length n0 (default: the current legal length); clamp k to this step."""
@@ -86,9 +116,10 @@ def prepare_request(batch: int, groups: int, capacity: int, *, valid_length: int
     offsets = row_offsets(batch, groups, capacity, device)
     fixed = torch.tensor(layout.fixed_positions(), dtype=torch.long, device=device)
     fixed = fixed.view(1, 1, -1).expand(batch, groups, -1).contiguous()
+    fixed_rows, off_lo = tag_standard_f((fixed + offsets).contiguous(), (offsets + layout.candidate_lo).contiguous(),
+                                        layout.candidate_lo, layout.candidate_hi, legal, capacity)
     return DecodeRequest(layout=layout, k0=k0, k=k, batch=batch, groups=groups, capacity=capacity, offsets=offsets,
-                         fixed_positions=fixed, fixed_rows=(fixed + offsets).contiguous(),
-                         off_lo=(offsets + layout.candidate_lo).contiguous())
+                         fixed_positions=fixed, fixed_rows=fixed_rows, off_lo=off_lo)
 
 
 def _layout_from_rows(fixed_rows, lo: int, hi: int, k: int, selected_count: int):
@@ -109,14 +140,14 @@ def _order(canonical_order: bool) -> str:
 def select_rows_kernel(u, zT, fixed_rows, off_lo, lo: int, hi: int, k: int) -> torch.Tensor:
     """D0: score the candidate columns from u, one top-k, merge with F. Returns flat int64 row ids [B*G*S].
 
-    F is regenerated from (lo, hi) by the selection rule (fixed_rows holds F + offsets in every caller of the
-    reference, decode.py:179-194, qwen_wrap.py:169-181); fixed_rows and off_lo are used for shapes only.
+    The kernel writes F from (lo, hi, legal); fixed_rows / off_lo must be the rule's F and offsets (check_standard_f).
     """
     B, G = fixed_rows.shape[:2]
     C = int(zT.shape[-1])
     if k <= 0:
         return fixed_rows.reshape(-1)
     legal = _layout_from_rows(fixed_rows, lo, hi, k, int(fixed_rows.shape[-1]) + k)
+    check_standard_f(fixed_rows, off_lo, lo, hi, legal, C)
     s = hip_score.candidate_scores(u, zT, lo, hi).view(B, G, hi - lo)
     _, flat = hip_select.select_rows(s, lo, hi, legal, k, C, order="score", want_flat=True)
     return flat
@@ -223,6 +254,7 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     legal = _layout_from_rows(fixed_rows, lo, hi, k, S)
     if legal > C:
         raise ValueError(f"legal length {legal} exceeds capacity {C}")
+    check_standard_f(fixed_rows, off_lo, lo, hi, legal, C)
     q = q_main.reshape(B, G, h, d).contiguous()
     q_cat = q_pre.reshape(B, G, h * d).contiguous()
     k_new = None

@@ -135,6 +135,19 @@ def model_views(K4, V4, q5, rows3):
 # ---------------------------------------------------------------------------------------------------------------------
 # batched forms
 # ---------------------------------------------------------------------------------------------------------------------
+def reference_attend(K, V, q, rows, *, scale=None):
+    """float32 CPU check of HipAttend from the same inputs (metal_attend.py:262-273): K/V [G,C,d], q [G,h,d], rows
+    [G,S] -> [G,h,d], softmax over the listed rows only, read by original position. Not a compute path."""
+    Kf, Vf, qf = (t.detach().float().cpu() for t in (K, V, q))
+    r = rows.detach().long().cpu()
+    sc = 1.0 / math.sqrt(K.shape[-1]) if scale is None else float(scale)
+    out = torch.empty(qf.shape)
+    for g in range(qf.shape[0]):
+        s = torch.einsum("id,sd->is", qf[g], Kf[g, r[g]]) * sc
+        out[g] = torch.softmax(s, dim=-1) @ Vf[g, r[g]]
+    return out
+
+
 _SHARED_WS = nat.Workspace()
 
 

@@ -313,6 +313,15 @@ def score_lightning_batched(keys, q, w, lo: int = 0, hi=None, *, q_pos0=None, re
     return out[..., :M]
 
 
+def reference_scores(zT, k_new, wk, q_cat, wq_t, lo: int, hi: int):
+    """float32 CPU check of HipScore.fused from the same inputs (metal_score.py:344-350): (u [G,r], z_new [G,r],
+    scores [G, hi-lo]). Not a compute path: the kernels above never call it."""
+    zf, kf, wkf, qf, wqf = (t.detach().float().cpu() for t in (zT, k_new, wk, q_cat, wq_t))
+    u = torch.einsum("gf,gfr->gr", qf, wqf)
+    z_new = torch.einsum("grd,gd->gr", wkf, kf)
+    return u, z_new, torch.einsum("gr,grm->gm", u, zf[:, :, int(lo):int(hi)])
+
+
 def scale_for(r: int) -> float:
     """The 1/sqrt(r) the reference folds into wq_t_scaled (indexer.py:45)."""
     return 1.0 / math.sqrt(r)

@@ -2,8 +2,12 @@
 
 Order contract, defined where torch.topk leaves ties unspecified: a larger score ranks first, equal scores rank by the
 lower candidate index, NaN ranks below every number, -0.0 equals +0.0. `topk` returns (values, indices) like
-torch.topk(..., sorted=True) on the last dimension; `select_rows` writes the whole row list of a decode step
-(F merged with the chosen candidates) in the layout the attend kernel reads.
+torch.topk(..., sorted=True) on the last dimension, for any k in either order; `select_rows` writes the whole row list
+of a decode step (F merged with the chosen candidates) in the layout the attend kernel reads.
+
+The tiled kernels' select state and scratch live in a module workspace that grows on demand and is never freed, so
+after one eager call of a shape the same calls allocate nothing and can be captured in a HIP graph. Calls that share it
+must be ordered on one stream (torch's current stream, where every call launches).
 """
 from __future__ import annotations
 
@@ -11,10 +15,11 @@ import torch
 
 from . import _native as nat
 
-MAX_SCORE_ORDER_K = 8192
+LDS_SORT_K = nat.LDS_SORT_K   # score order up to this k is sorted in LDS; past it, by a radix pass (tiled entry)
 TILED_MIN_M = 32768     # rows at least this long are selected by the tiled kernels (attnlab_topk_tiled)
 TILED_MAX_M = 262144    # ... and at most this long (longer rows take the single-workgroup select)
 ORDERS = {"position": nat.ORDER_POSITION, "score": nat.ORDER_SCORE}
+_WS = nat.Workspace()   # select state (zeroed once, left zeroed by every call) and scratch, per device
 
 
 def _order_code(order) -> int:
@@ -28,7 +33,8 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
 
     order="score": descending score, ties lowest index first (torch.topk's sorted order with ties defined);
     order="position": the same set, indices ascending. tiled: None picks the tiled kernels for rows of
-    TILED_MIN_M..TILED_MAX_M scores, True / False forces the choice (same result either way).
+    TILED_MIN_M..TILED_MAX_M scores (and for score order past LDS_SORT_K, which needs their scratch), True / False
+    forces the choice where both apply (same result either way).
     """
     if scores.dtype != torch.float32 or not scores.is_cuda:
         raise ValueError("scores must be a float32 tensor on a HIP device")
@@ -39,8 +45,6 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
     k = int(k)
     if not 0 <= k <= M:
         raise ValueError(f"need 0 <= k <= {M}, got {k}")
-    if code == nat.ORDER_SCORE and k > MAX_SCORE_ORDER_K:
-        raise ValueError(f"score order supports k <= {MAX_SCORE_ORDER_K}")
     lead = tuple(scores.shape[:-1])
     s2 = scores.reshape(-1, M)
     if s2.stride(-1) != 1:
@@ -50,12 +54,14 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
     val = torch.empty(R, max(k, 1), dtype=torch.float32, device=scores.device)
     if tiled is None:
         tiled = TILED_MIN_M <= M <= TILED_MAX_M
+    if code == nat.ORDER_SCORE and k > LDS_SORT_K:
+        tiled = True   # the radix pass of a long score order runs in the tiled entry's scratch
     if R and k and tiled:
-        state = torch.zeros(R, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=scores.device)
-        nbytes = nat.lib().attnlab_select_scratch_bytes(R, M)
-        scratch = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=scores.device)
+        state = _WS.bytes(scores.device, R * nat.SELECT_STATE_WORDS * 4, "state")
+        nbytes = nat.lib().attnlab_select_scratch_bytes(R, M, k, code)
+        scratch = _WS.bytes(scores.device, nbytes, "scratch")
         nat.call("attnlab_topk_tiled", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
-                 idx.stride(0), state.data_ptr(), scratch.data_ptr(), nbytes, nat.stream_of(scores.device))
+                 idx.stride(0), state.data_ptr(), scratch.data_ptr(), scratch.numel(), nat.stream_of(scores.device))
     elif R and k:
         nat.call("attnlab_topk", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
                  idx.stride(0), nat.stream_of(scores.device))
@@ -71,7 +77,7 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
     first and then the candidates by descending score, like cat(fixed_rows, topk.indices) in decode.py:93.
     state: the select state score_grouped(..., state=) filled for these scores (cleared here), or None. With a state
     and tiled=True the keys are classified by a grid of 4096-key tiles and each row resolved by one workgroup (same
-    result as the single-workgroup select, in either order).
+    result as the single-workgroup select, in either order). Score order takes any k.
     """
     if scores.dim() != 3 or scores.dtype != torch.float32 or not scores.is_cuda or scores.stride(2) != 1:
         raise ValueError("scores must be a float32 [B, G, M] tensor with unit column stride on a HIP device")
@@ -99,9 +105,9 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
                               or not state.is_contiguous() or state.device != scores.device):
         raise ValueError(f"state must be a contiguous int32 [{B}, {G}, {W}] tensor on the scores' device")
     scratch = None
-    if state is not None and tiled and k > 0:
-        nbytes = nat.lib().attnlab_select_scratch_bytes(B * G, M)
-        scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=scores.device)
+    if k > 0 and ((state is not None and tiled) or (code == nat.ORDER_SCORE and k > LDS_SORT_K)):
+        nbytes = nat.lib().attnlab_select_scratch_bytes(B * G, M, k, code)
+        scratch = _WS.bytes(scores.device, nbytes, "scratch")
     nat.call("attnlab_select_rows", scores.data_ptr(), stride, B, G, lo, hi, legal, k, capacity, code,
              rows.data_ptr(), S, nat.ptr(flat), nat.ptr(state), nat.ptr(scratch),
              0 if scratch is None else scratch.numel(), nat.stream_of(scores.device))

@@ -71,3 +71,13 @@ class GroupedIndexer:
 
     def scores(self, u: torch.Tensor, zT: torch.Tensor, lo: int = 0, hi=None) -> torch.Tensor:
         return candidate_scores(u, zT, lo, zT.shape[-1] if hi is None else hi)
+
+    def reference_scores(self, q_pre: torch.Tensor, k_pre: torch.Tensor, lo: int = 0, hi=None) -> torch.Tensor:
+        """float64 CPU brute force from the stored weights (indexer.py:57-64): scores [B,G,T,hi-lo] of the T queries
+        q_pre [B,G,h,T,d] against the keys k_pre [B,G,C,d], (wq . concat_h q)(wk . k) / sqrt(r) over [lo, hi)."""
+        B, G, h, T, d = q_pre.shape
+        hi = int(k_pre.shape[2]) if hi is None else int(hi)
+        q_cat = q_pre.detach().double().cpu().permute(0, 1, 3, 2, 4).reshape(B, G, T, h * d)
+        u = torch.einsum("bgtf,grf->bgtr", q_cat, self.wq.detach().double().cpu())
+        z = torch.einsum("grd,bgcd->bgrc", self.wk.detach().double().cpu(), k_pre.detach().double().cpu()[:, :, lo:hi])
+        return torch.einsum("bgtr,bgrc->bgtc", u, z) / math.sqrt(self.r)

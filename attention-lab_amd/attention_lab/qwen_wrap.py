@@ -28,7 +28,8 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from .decode import gathered_decode_step_kernel, select_rows_recent, select_rows_uniform, sparse_decode_step_kernel
+from .decode import (gathered_decode_step_kernel, select_rows_recent, select_rows_uniform, sparse_decode_step_kernel,
+                     tag_standard_f)
 from .full import full_attention
 from .indexer import GroupedIndexer, project_keys
 from .selection import FIXED_PREFIX, FIXED_RECENT, fixed_budget, selection_layout
@@ -178,6 +179,7 @@ def build_step_plan(cache: LabCache, legal_length: int, k0: int) -> StepPlan:
         pos = torch.tensor(layout.fixed_positions(), dtype=torch.long, device=cache.device).view(1, 1, -1)
         fixed_rows = (pos + cache.offsets).contiguous()
         off_lo = (cache.offsets + layout.candidate_lo).contiguous()
+    tag_standard_f(fixed_rows, off_lo, layout.candidate_lo, layout.candidate_hi, int(legal_length), cache.slots)
     return StepPlan(legal_length=int(legal_length), k0=int(k0), k=int(k), lo=layout.candidate_lo,
                     hi=layout.candidate_hi, fixed_count=layout.fixed_count, selected_count=layout.fixed_count + k,
                     fixed_rows=fixed_rows, off_lo=off_lo)

@@ -3,7 +3,8 @@
 Same names as the reference's sparse module (src/attention_lab/sparse.py:14-67). The reference reads a subset by
 materialising it (index_select of K and V rows, then SDPA over the copies); here `gather_attention` hands the
 position list to the attend kernel, which reads each listed K/V row straight from the cache. `gather_rows` is kept as
-a data-movement utility (the reference's tests use it to check that positions are original).
+a data-movement utility (the reference's tests use it to check that positions are original), and `subset_attention`
+attends over such an already gathered subset on the same kernel (its rows are the subset's own slots).
 """
 from __future__ import annotations
 
@@ -52,3 +53,31 @@ def gather_attention(q, k, v, selected, selected_valid=None, *, scale=None, back
     pos = pos.to(torch.int32).contiguous()
     out = hip_attend.attend(q.reshape(B, G, h, d).contiguous(), k, v, pos, scale=scale, out_dtype=q.dtype)
     return out.view(B, G, h, 1, d)
+
+
+def subset_attention(q, k_sub, v_sub, valid_mask=None, *, scale=None, backend="sdpa"):
+    """Attention of q [B,G,h,T,d] over a gathered subset k_sub, v_sub [B,G,S,d] -> [B,G,h,T,d] (sparse.py:40-60).
+
+    The h*T query rows of a group share the S subset rows (each row is read once per group), so the T queries fold
+    into the head axis of the attend kernel: h*T <= 8 rows per group, bfloat16, d = 128. valid_mask [B,G,S] (bool)
+    drops padded slots; a group with no valid slot has no defined output.
+    """
+    if backend not in ("sdpa", "explicit"):
+        raise ValueError(f"unknown subset backend {backend!r}")
+    if q.dim() != 5 or k_sub.dim() != 4 or v_sub.shape != k_sub.shape:
+        raise ValueError("q must be [B,G,h,T,d] and k_sub, v_sub [B,G,S,d]")
+    B, G, h, T, d = q.shape
+    S = int(k_sub.shape[2])
+    if tuple(k_sub.shape[:2]) != (B, G) or k_sub.shape[3] != d:
+        raise ValueError(f"subset {tuple(k_sub.shape)} does not match q {tuple(q.shape)}")
+    if h * T > hip_attend.MAX_H:
+        raise ValueError(f"h*T = {h * T} query rows per group exceed the kernel's {hip_attend.MAX_H}")
+    slots = torch.arange(S, device=k_sub.device, dtype=torch.int32).expand(B, G, S)
+    if valid_mask is not None:
+        if tuple(valid_mask.shape) != (B, G, S):
+            raise ValueError(f"valid_mask must be [B,G,S] = [{B},{G},{S}]")
+        slots = torch.where(valid_mask.bool(), slots, torch.full_like(slots, -1))
+    qf = q.reshape(B, G, h * T, d).contiguous()
+    out = hip_attend.attend(qf, k_sub.contiguous(), v_sub.contiguous(), slots.contiguous(), scale=scale,
+                            out_dtype=q.dtype)
+    return out.view(B, G, h, T, d)

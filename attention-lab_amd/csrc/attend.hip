@@ -172,7 +172,11 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
                 }
             }
             float vf[16];
-            const uint32_t vw[8] = {s.v0.x, s.v0.y, s.v0.z, s.v0.w, s.v1.x, s.v1.y, s.v1.z, s.v1.w};
+            // a masked entry loaded row 0 in its place: its V words are zeroed so that a non-finite row 0 (a padded
+            // slot of a gathered subset, say) cannot turn its zero weight into NaN
+            const uint32_t vm = s.ok ? 0xffffffffu : 0u;
+            const uint32_t vw[8] = {s.v0.x & vm, s.v0.y & vm, s.v0.z & vm, s.v0.w & vm,
+                                    s.v1.x & vm, s.v1.y & vm, s.v1.z & vm, s.v1.w & vm};
 #pragma unroll
             for (int w = 0; w < 8; ++w) {
                 vf[2 * w] = bf16_lo(vw[w]);

@@ -16,8 +16,9 @@ struct Layout {
     int64_t score_stride;
 };
 
-// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | tiled-select scratch |
-// partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state (first-digit histograms and
+// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | select scratch (the
+// tiled select's bitmaps and candidate entries, and for k past the LDS sort the score-order sort's buffers, sized for
+// score order so either order fits) | partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state (first-digit histograms and
 // candidate counters, which must start at zero) lives in its own buffer: a region inside this shape-dependent layout
 // would overlap other data of a differently shaped earlier call.
 Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
@@ -30,7 +31,7 @@ Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     L.rows = align_up(k > 0 ? BG * L.score_stride * 4 : 0);
     L.u = L.rows + align_up(BG * S * 4);
     L.sel = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
-    L.part = L.sel + align_up(k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M) : 0);
+    L.part = L.sel + align_up(k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M, k, ATTNLAB_ORDER_SCORE) : 0);
     L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
     return L;
 }
@@ -61,6 +62,13 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     ATTNLAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, "workspace of %lld bytes needed, got %lld",
                     (long long)L.total, (long long)workspace_bytes);
     ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, "workspace must be 256-byte aligned");
+    // every check of the select before the first launch: the score kernel adds into the select state, which only the
+    // select clears, so a call rejected after the score launch would leave it dirty for the next call
+    {
+        const int rc0 = select_check(B, G, lo, hi, legal, k, C, order, rows_out, lo + (legal - hi) + k,
+                                     reinterpret_cast<const float*>(workspace), L.score_stride);
+        if (rc0) return rc0;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
     if (k == 0) state = nullptr;

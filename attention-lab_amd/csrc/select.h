@@ -55,14 +55,20 @@ __device__ __forceinline__ void clear_histogram(uint32_t* hsh) {
     for (int b = threadIdx.x; b < kHistBins; b += BLOCK) hsh[b] = 0u;
 }
 
+// The argument checks of attnlab_select_rows (the decode step runs them before its first launch, so a rejected call
+// leaves the select state untouched).
+int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
+                 int64_t rows_stride, const float* scores, int64_t score_stride);
+
 // attnlab_select_rows: `state` [B*G][kSelectStateWords] (nullable) holds the first-digit histograms the score kernel
-// built; with it and a scratch of select_scratch_bytes(B*G, M) the position-order select runs tiled over the chip.
+// built; with it and a scratch of select_scratch_bytes(B*G, M, k, order) the select runs tiled over the chip.
 int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
                      int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
                      void* scratch, int64_t scratch_bytes, hipStream_t stream);
 
-// Scratch bytes of the tiled select for R rows of M candidates (no zeroing needed).
-int64_t select_scratch_bytes(int R, int M);
+// Scratch bytes of the tiled select for R rows of M candidates, plus the score-order sort's buffers when order is
+// score order and k exceeds what the LDS sort holds (no zeroing needed).
+int64_t select_scratch_bytes(int R, int M, int k, int order);
 
 // attnlab_score_grouped with an optional select-state output: per row, the first-digit histogram of the scores.
 int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,

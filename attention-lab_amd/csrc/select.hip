@@ -901,7 +901,398 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
     finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
 }
 
-static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStream_t s, bool build_hist = false) {
+// ---------------------------------------------------------------------------------------------------------------
+// Compact tiled select, rows of at most kCompactMaxTiles tiles (M <= 32768, the decode step's 32K context):
+//   A select_classify_compact  as select_classify, but instead of a candidate bitmap each wave writes its candidates
+//                              (first digit == b1) as (index, low 21 key bits) entries, in index order, into a region
+//                              of its own (no barrier, no atomic), with (above, candidate) counts beside it.
+//   B select_resolve_compact   one round trip loads the row's above bitmap, the region counts and the entries; the two
+//                              remaining digits are searched on the entries' low key bits, the chosen candidates are
+//                              ORed into the bitmap and the set bits emitted as in select_resolve. No candidate list is
+//                              built and no score is gathered. A wave region that overflowed sends the row to the
+//                              single-workgroup streaming select.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kCompactMaxTiles = 8;
+constexpr int kCompactWaves = kTileThreads / 64;                         // regions per tile
+constexpr int kCompactRegions = kCompactMaxTiles * kCompactWaves;        // 32 per row
+constexpr int kCompactWaveCap = 128;                                     // entries per region (a wave's 1024 keys)
+constexpr int kCompactEntries = kCompactRegions * kCompactWaveCap;       // 4096 per row
+constexpr int kCompactPerThread = kCompactEntries / kSelThreads;         // 4 entries per resolve thread
+constexpr int kCompactWords = kCompactMaxTiles * kTileKeys / 32;         // 1024 bitmap words: one per resolve thread
+static_assert(kCompactPerThread == 4 && kCompactWords == kSelThreads, "resolve layout");
+static_assert(kCompactWaveCap % kCompactPerThread == 0, "a thread's entries lie in one region");
+
+struct CompactArgs {
+    uint32_t* above;   // [R, W] bit i: key i's first digit > b1
+    uint2* counts;     // [R, kCompactRegions] (keys above b1, candidates) of each classify wave
+    uint2* entries;    // [R, kCompactRegions, kCompactWaveCap] (candidate index, low 21 bits of its key)
+    int W, T;
+};
+
+__host__ __device__ inline int64_t align_bytes(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// Per-row byte layout of the compact scratch: the above bitmap, the counts, the entries (16-byte aligned parts).
+__host__ __device__ inline int64_t compact_bitmap_bytes(int M) { return align_bytes(((int64_t)M + 31) / 32 * 4, 16); }
+__host__ __device__ inline int64_t compact_row_bytes(int M) {
+    return compact_bitmap_bytes(M) + (int64_t)kCompactRegions * 8 + (int64_t)kCompactEntries * 8;
+}
+
+__host__ __device__ inline bool compact_fits(int M) { return M <= kCompactMaxTiles * kTileKeys; }
+
+// Scratch of the tiled select (either form) for R rows of M candidates.
+__host__ __device__ inline int64_t tiled_region_bytes(int R, int M) {
+    return compact_fits(M) ? (int64_t)R * compact_row_bytes(M) : tiled_scratch_bytes(R, M);
+}
+
+__global__ __launch_bounds__(kTileThreads) void select_classify_compact(SelectArgs a, CompactArgs t) {
+    const int lin = xcd_contiguous_block();
+    const int row = lin / t.T, tile = lin - row * t.T;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* s = a.scores + (size_t)row * a.score_stride;
+    const int i0 = tile * kTileKeys + tid * kTileKPT;
+    float v[kTileKPT];
+    const int nvalid = load_tile_scores(s, i0, a.M, v);
+    const uint32_t b1 = first_digit_2level(a.hist + (size_t)row * kSelectStateWords, (uint32_t)a.k);
+    uint32_t abits = 0, cbits = 0, low[kTileKPT];
+#pragma unroll
+    for (int i = 0; i < kTileKPT; ++i) {
+        const uint32_t key = score_key(v[i]);
+        const uint32_t dg = key >> kHistShift;
+        low[i] = key & ((1u << kHistShift) - 1u);
+        if (i < nvalid) {
+            abits |= (uint32_t)(dg > b1) << i;
+            cbits |= (uint32_t)(dg == b1) << i;
+        }
+    }
+    // above bitmap: two threads per 32-bit word, the even thread's keys in the low half
+    const uint32_t an = __shfl_xor(abits, 1, 64);
+    const int w = tile * (kTileKeys / 32) + (tid >> 1);
+    if ((tid & 1) == 0 && w < t.W) t.above[(size_t)row * t.W + w] = abits | (an << 16);
+    // this wave's candidates, lane after lane (index order), from the packed inclusive scan of (above << 16 | cand)
+    // (each field's wave total is at most 1024, so the halves never carry into each other)
+    const uint32_t na = (uint32_t)__popc(abits), nc = (uint32_t)__popc(cbits);
+    const uint32_t inc = wave_incl_scan((na << 16) | nc);
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    const int region = tile * kCompactWaves + wave;
+    uint2* ent = t.entries + ((size_t)row * kCompactRegions + region) * kCompactWaveCap;
+    uint32_t slot = (inc & 0xffffu) - nc;
+    uint32_t bits = cbits;
+    while (bits) {
+        const int i = __ffs(bits) - 1;
+        bits &= bits - 1;
+        if (slot < (uint32_t)kCompactWaveCap) ent[slot] = make_uint2((uint32_t)(i0 + i), low[i]);
+        ++slot;
+    }
+    if (lane == 0) t.counts[(size_t)row * kCompactRegions + region] = make_uint2(tot >> 16, tot & 0xffffu);
+}
+
+// Emission of a selection bitmap held one word per thread (word tid of the row; slot = this thread's first output
+// slot), then F and the cleared state. Shared by select_resolve_compact's position and score orders.
+__device__ __forceinline__ void emit_word_row(const SelectArgs& a, int row, SelectShared& sh, uint32_t word,
+                                              uint32_t slot) {
+    const int tid = threadIdx.x;
+    uint32_t* st = a.hist + (size_t)row * kSelectStateWords;   // leave the histogram zeroed for the next call
+    if (a.order == ATTNLAB_ORDER_POSITION && !a.top_idx && !a.top_val) {
+        const int nrec = a.legal - a.hi, S = a.lo + nrec + a.k, nf = a.lo + nrec;
+        int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride : nullptr;
+        int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S : nullptr;
+        const int64_t base = (int64_t)row * a.C;
+        while (word) {
+            const uint32_t b = __ffs(word) - 1;
+            word &= word - 1;
+            const int idx = tid * 32 + (int)b;
+            if (slot < (uint32_t)a.k) {
+                if (rows) rows[a.lo + slot] = a.lo + idx;
+                if (flat) flat[a.lo + slot] = base + a.lo + idx;
+            }
+            ++slot;
+        }
+        for (int f = tid; f < nf; f += kSelThreads) {
+            const int p = f < a.lo ? f : a.hi + (f - a.lo);
+            const int s_out = f < a.lo ? f : a.lo + a.k + (f - a.lo);
+            if (rows) rows[s_out] = p;
+            if (flat) flat[s_out] = base + p;
+        }
+        for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
+        return;
+    }
+    const Emitter em = make_emitter(a, row, sh);
+    const bool by_score = a.order == ATTNLAB_ORDER_SCORE;
+    const float* srow = a.scores + (size_t)row * a.score_stride;
+    while (word) {
+        const uint32_t b = __ffs(word) - 1;
+        word &= word - 1;
+        const int idx = tid * 32 + (int)b;
+        em.put(slot++, idx, by_score ? score_key(srow[idx]) : 0u);
+    }
+    for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
+    __syncthreads();
+    finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_resolve_compact(SelectArgs a, CompactArgs t) {
+    __shared__ SelectShared sh;   // hist: the second digit's histogram; sortbuf: score order's staged pairs
+    // the third digit's histogram and the selection bitmap, or the streaming fallback's histograms and bitmaps
+    __shared__ __attribute__((aligned(16))) uint32_t lds[2048 + 1024 + 2 * kRegWords];
+    __shared__ uint32_t totals[2];   // keys above b1, overflow flag
+    uint32_t* hist3 = lds;
+    uint32_t* bits = lds + 1024;
+    const int row = xcd_contiguous_block();   // the XCD that classified the row
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nreg = kCompactWaves * t.T;
+    // one round trip: this thread's bitmap word, its four entries and their region's count (wave 0: every count)
+    const int e0 = kCompactPerThread * tid;
+    const int reg = e0 / kCompactWaveCap, slot0 = e0 - reg * kCompactWaveCap;
+    const uint32_t aw = tid < t.W ? t.above[(size_t)row * t.W + tid] : 0u;
+    uint4 p01 = make_uint4(0, 0, 0, 0), p23 = make_uint4(0, 0, 0, 0);
+    uint2 rc = make_uint2(0, 0), wc = make_uint2(0, 0);
+    if (reg < nreg) {
+        const uint4* ep = reinterpret_cast<const uint4*>(t.entries + (size_t)row * kCompactEntries + e0);
+        p01 = ep[0];
+        p23 = ep[1];
+        rc = t.counts[(size_t)row * kCompactRegions + reg];
+    }
+    if (wave == 0 && lane < nreg) wc = t.counts[(size_t)row * kCompactRegions + lane];
+    sh.hist[tid] = 0u;
+    sh.hist[tid + kSelThreads] = 0u;
+    hist3[tid] = 0u;
+    bits[tid] = aw;
+    if (wave == 0) {
+        uint32_t na = wc.x;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) na += __shfl_xor(na, o, 64);
+        const bool over = __ballot(wc.y > (uint32_t)kCompactWaveCap) != 0;
+        if (lane == 0) {
+            totals[0] = na;
+            totals[1] = over;
+            sh.digit = 0u;   // defaults keep every later index in range even for a state that does not match the scores
+            sh.krem = 0u;
+            sh.dcount = 0u;
+        }
+    }
+    __syncthreads();
+    if (totals[1]) {   // a wave region overflowed: the single-workgroup select over the row's scores
+        select_row_streaming(a, row, sh, StreamLds{lds, lds + 2048, lds + 3072, lds + 3072 + kRegWords});
+        return;
+    }
+    uint32_t krem = (uint32_t)a.k - totals[0];   // candidates to take, 1 <= krem <= candidates
+    const uint32_t ex[4] = {p01.x, p01.z, p23.x, p23.z}, ey[4] = {p01.y, p01.w, p23.y, p23.w};
+    bool ev[4];
+    uint32_t eidx[4], elow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        ev[j] = reg < nreg && (uint32_t)(slot0 + j) < rc.y;
+        eidx[j] = ev[j] ? min(ex[j], (uint32_t)a.M - 1u) : 0u;
+        elow[j] = ey[j] & ((1u << kHistShift) - 1u);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (ev[j]) atomicAdd(&sh.hist[elow[j] >> 10], 1u);
+    __syncthreads();
+    find_digit_wave(sh, sh.hist, krem, 2048);
+    const uint32_t d2 = sh.digit & 2047u;
+    krem = sh.krem;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (ev[j] && (elow[j] >> 10) == d2) atomicAdd(&hist3[elow[j] & 1023u], 1u);
+    __syncthreads();
+    find_digit_wave(sh, hist3, krem, 1024);
+    const uint32_t tlow = (d2 << 10) | (sh.digit & 1023u);
+    krem = sh.krem;
+    if (sh.dcount <= krem) {
+        // every key equal to the threshold is taken (the usual case: no tie at the boundary)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (ev[j] && elow[j] >= tlow) atomicOr(&bits[eidx[j] >> 5], 1u << (eidx[j] & 31u));
+    } else {
+        // equal keys at the threshold: the first krem of them in index order. Regions follow the index order (tile
+        // after tile, wave after wave), entries inside a region too, and thread t holds entries 4t..4t+3, so a block
+        // scan of the tied counts ranks the ties by index.
+        uint32_t neq = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) neq += ev[j] && elow[j] == tlow;
+        uint32_t eeq, unused, teq, unused_t;
+        block_scan2<kSelThreads>(neq, 0u, eeq, unused, teq, unused_t, sh.wave_tot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!ev[j]) continue;
+            const bool eq = elow[j] == tlow;
+            if (elow[j] > tlow || (eq && eeq < krem)) atomicOr(&bits[eidx[j] >> 5], 1u << (eidx[j] & 31u));
+            eeq += eq;
+        }
+    }
+    __syncthreads();
+    init_sortbuf(a, sh);   // score order: the staged pairs' padding, ordered by the scan's barriers
+    const uint32_t sw = tid < t.W ? bits[tid] : 0u;
+    uint32_t slot, unused2, tsel, unused_t2;
+    block_scan2<kSelThreads>((uint32_t)__popc(sw), 0u, slot, unused2, tsel, unused_t2, sh.wave_tot);
+    emit_word_row(a, row, sh, sw, slot);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Score order past kMaxScoreOrderK, where the k selected pairs no longer fit the LDS sort: the select runs in position
+// order into `stage` (candidate indices, ascending), then select_sort_score lists them by descending score with three
+// stable LSD radix passes over the order-preserving key (digits of 10, 11 and 11 bits, each complemented so that
+// ascending digit order is descending score). Stability keeps equal scores in ascending index order, as the LDS sort
+// does. One 1024-thread workgroup per row. A pass counts its digit over the row (LDS histogram; its exclusive scan is
+// each digit's first slot), then places the row 1024 elements at a time: a lane's rank among the lanes of its wave
+// with the same digit comes from one ballot per digit bit, the earlier waves' counts of that digit from an LDS table,
+// the earlier tiles' from a running count. Elements move as (key << 32 | index) through two scratch buffers; the last
+// pass writes the outputs and F.
+// ---------------------------------------------------------------------------------------------------------------
+struct SortScratch {
+    int32_t* stage;   // [R, k] the position-order select's candidate indices
+    uint64_t* buf0;   // [R, k]
+    uint64_t* buf1;   // [R, k]
+};
+
+__host__ __device__ inline int64_t sort_scratch_bytes(int R, int k) {
+    return align_bytes((int64_t)R * k * 4, 256) + 2 * align_bytes((int64_t)R * k * 8, 256);
+}
+
+__host__ __device__ inline bool staged_score_order(int order, int k) {
+    return order == ATTNLAB_ORDER_SCORE && k > kMaxScoreOrderK;
+}
+
+struct SortShared {
+    uint16_t cnt[kSelWaves][kHistBins];   // this tile's count of each digit per wave, zero between tiles
+    uint32_t base[kHistBins];             // first slot of each digit in this pass
+    uint32_t run[kHistBins];              // elements of each digit placed by the earlier tiles
+    uint32_t wave_tot[kSelWaves][2];
+};
+
+__global__ __launch_bounds__(kSelThreads) void select_sort_score(SelectArgs a, SortScratch sc) {
+    __shared__ SortShared sh;
+    const int row = xcd_contiguous_block();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k = a.k;
+    const float* srow = a.scores + (size_t)row * a.score_stride;
+    const int32_t* stage = sc.stage + (size_t)row * k;
+    uint64_t* b0 = sc.buf0 + (size_t)row * k;
+    uint64_t* b1 = sc.buf1 + (size_t)row * k;
+    const int nrec = a.legal - a.hi, nf = a.lo + nrec, S = nf + k;
+    int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride : nullptr;
+    int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S : nullptr;
+    int32_t* ti = a.top_idx ? a.top_idx + (size_t)row * a.top_stride : nullptr;
+    float* tv = a.top_val ? a.top_val + (size_t)row * a.top_stride : nullptr;
+    const int64_t base = (int64_t)row * a.C;
+    for (int i = tid; i < kSelWaves * kHistBins / 2; i += kSelThreads) reinterpret_cast<uint32_t*>(&sh.cnt[0][0])[i] = 0u;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = pass == 0 ? 0 : (pass == 1 ? 10 : 21);
+        const int nbits = pass == 0 ? 10 : 11;
+        const uint32_t dmask = (1u << nbits) - 1u;
+        // pass 0: stage (keys gathered) -> b1 -> b0; pass 1: b0 -> b1; pass 2: b1 -> outputs
+        const uint64_t* src = pass == 1 ? b0 : b1;
+        uint64_t* dst = pass == 0 ? b0 : b1;
+        sh.base[tid] = 0u;
+        sh.base[tid + kSelThreads] = 0u;
+        sh.run[tid] = 0u;
+        sh.run[tid + kSelThreads] = 0u;
+        __syncthreads();
+        for (int e = tid; e < k; e += kSelThreads) {
+            uint64_t x;
+            if (pass == 0) {
+                const uint32_t idx = (uint32_t)min(max(stage[e], 0), a.M - 1);
+                x = ((uint64_t)score_key(srow[idx]) << 32) | idx;
+                b1[e] = x;
+            } else {
+                x = src[e];
+            }
+            atomicAdd(&sh.base[dmask - (((uint32_t)(x >> 32) >> shift) & dmask)], 1u);
+        }
+        __syncthreads();
+        {   // exclusive scan of the digit counts (two bins per thread; the second is 0 past nbins)
+            const uint32_t c0 = sh.base[2 * tid], c1 = sh.base[2 * tid + 1];
+            uint32_t ex, unused, tot, unused_t;
+            block_scan2<kSelThreads>(c0 + c1, 0u, ex, unused, tot, unused_t, sh.wave_tot);
+            sh.base[2 * tid] = ex;
+            sh.base[2 * tid + 1] = ex + c0;
+        }
+        __syncthreads();
+        for (int t0 = 0; t0 < k; t0 += kSelThreads) {
+            const int e = t0 + tid;
+            const bool ok = e < k;
+            const uint64_t x = ok ? src[e] : 0ull;
+            const uint32_t dg = dmask - (((uint32_t)(x >> 32) >> shift) & dmask);
+            uint64_t peers = __ballot(ok);
+            for (int b = 0; b < nbits; ++b) {
+                const bool bit = (dg >> b) & 1u;
+                const uint64_t m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            const bool leader = ok && (peers & lt) == 0;
+            const uint32_t n = (uint32_t)__popcll(peers);
+            if (leader) sh.cnt[wave][dg] = (uint16_t)n;
+            __syncthreads();
+            uint32_t off = 0u;
+            if (leader) {
+                off = sh.base[dg] + sh.run[dg];
+                for (int w = 0; w < wave; ++w) off += sh.cnt[w][dg];
+            }
+            const int src_lane = ok ? __ffsll((unsigned long long)peers) - 1 : lane;
+            off = (uint32_t)__shfl((int)off, src_lane, 64);
+            const uint32_t slot = off + (uint32_t)__popcll(peers & lt);
+            if (ok && slot < (uint32_t)k) {
+                if (pass < 2) {
+                    dst[slot] = x;
+                } else {
+                    const int idx = (int)(uint32_t)x;
+                    if (ti) ti[slot] = idx;
+                    if (tv) tv[slot] = srow[idx];
+                    if (rows) rows[nf + slot] = a.lo + idx;
+                    if (flat) flat[nf + slot] = base + a.lo + idx;
+                }
+            }
+            __syncthreads();
+            if (leader) {
+                sh.cnt[wave][dg] = 0;
+                atomicAdd(&sh.run[dg], n);
+            }
+        }
+        __syncthreads();
+    }
+    for (int f = tid; f < nf; f += kSelThreads) {   // F first, ascending (cat(fixed_rows, topk) of decode.py:93)
+        const int p = f < a.lo ? f : a.hi + (f - a.lo);
+        if (rows) rows[f] = p;
+        if (flat) flat[f] = base + p;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------------------------------
+// Bytes of the scratch: the tiled select's region, then (score order past kMaxScoreOrderK) the sort's stage and buffers.
+int64_t select_scratch_bytes(int R, int M, int k, int order) {
+    int64_t b = align_bytes(tiled_region_bytes(R, M), 256);
+    if (staged_score_order(order, k)) b += sort_scratch_bytes(R, k);
+    return b;
+}
+
+static int launch_tiled(const SelectArgs& a, int R, void* scratch, hipStream_t s, bool build_hist) {
+    const int W = (a.M + 31) / 32, T = (a.M + kTileKeys - 1) / kTileKeys;
+    if (compact_fits(a.M)) {
+        CompactArgs c;
+        char* p = static_cast<char*>(scratch);
+        c.above = reinterpret_cast<uint32_t*>(p);
+        c.counts = reinterpret_cast<uint2*>(p + (size_t)R * compact_bitmap_bytes(a.M));
+        c.entries = c.counts + (size_t)R * kCompactRegions;
+        c.W = W;
+        c.T = T;
+        // above is [R, W] (rows W words apart) inside the first R * compact_bitmap_bytes(M) bytes
+        if (build_hist) {
+            TiledArgs th{c.above, nullptr, W, T};
+            hipLaunchKernelGGL(select_hist, dim3(R * T), dim3(kTileThreads), 0, s, a, th);
+        }
+        hipLaunchKernelGGL(select_classify_compact, dim3(R * T), dim3(kTileThreads), 0, s, a, c);
+        hipLaunchKernelGGL(select_resolve_compact, dim3(R), dim3(kSelThreads), 0, s, a, c);
+        return check_launch("select_compact");
+    }
+    TiledArgs t;
+    t.above = static_cast<uint32_t*>(scratch);
+    t.cand = t.above + (size_t)R * W;
+    t.W = W;
+    t.T = T;
     if (build_hist) hipLaunchKernelGGL(select_hist, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
     hipLaunchKernelGGL(select_classify, dim3(R * t.T), dim3(kTileThreads), 0, s, a, t);
     if (a.M >= kCandCapLongFromM) hipLaunchKernelGGL(select_resolve<kCandCapLong>, dim3(R), dim3(kSelThreads), 0, s, a, t);
@@ -909,39 +1300,67 @@ static int launch_tiled(const SelectArgs& a, const TiledArgs& t, int R, hipStrea
     return check_launch("select_tiled");
 }
 
-int64_t select_scratch_bytes(int R, int M) { return tiled_scratch_bytes(R, M); }
+// The selection of R rows with `a` (its outputs and order), run tiled when `tiled`, else one workgroup per row; score
+// order past kMaxScoreOrderK goes through the position-order select into the sort's stage and select_sort_score.
+static int run_select(const SelectArgs& a, int R, bool tiled, void* scratch, hipStream_t s, bool build_hist) {
+    SelectArgs sel = a;
+    SortScratch sc{};
+    const bool staged = staged_score_order(a.order, a.k);
+    if (staged) {
+        char* p = static_cast<char*>(scratch) + align_bytes(tiled_region_bytes(R, a.M), 256);
+        sc.stage = reinterpret_cast<int32_t*>(p);
+        sc.buf0 = reinterpret_cast<uint64_t*>(p + align_bytes((int64_t)R * a.k * 4, 256));
+        sc.buf1 = reinterpret_cast<uint64_t*>(p + align_bytes((int64_t)R * a.k * 4, 256) +
+                                              align_bytes((int64_t)R * a.k * 8, 256));
+        sel.order = ATTNLAB_ORDER_POSITION;
+        sel.rows = nullptr;
+        sel.rows_flat = nullptr;
+        sel.top_idx = sc.stage;
+        sel.top_val = nullptr;
+        sel.top_stride = a.k;
+    }
+    const int rc = tiled ? launch_tiled(sel, R, scratch, s, build_hist) : launch_select(sel, R, s);
+    if (rc || !staged) return rc;
+    hipLaunchKernelGGL(select_sort_score, dim3(R), dim3(kSelThreads), 0, s, a, sc);
+    return check_launch("select_sort_score");
+}
 
-int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
-                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
-                     void* scratch, int64_t scratch_bytes, hipStream_t stream) {
+int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
+                 int64_t rows_stride, const float* scores, int64_t score_stride) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
                     lo, hi, legal, C);
     const int M = hi - lo;
     ATTNLAB_REQUIRE(0 <= k && k <= M, "need 0 <= k <= hi - lo, got k=%d M=%d", k, M);
     ATTNLAB_REQUIRE(order == ATTNLAB_ORDER_POSITION || order == ATTNLAB_ORDER_SCORE, "unknown order %d", order);
-    ATTNLAB_REQUIRE(order != ATTNLAB_ORDER_SCORE || k <= kMaxScoreOrderK, "score order supports k <= %d, got %d",
-                    kMaxScoreOrderK, k);
     const int S = lo + (legal - hi) + k;
     ATTNLAB_REQUIRE(S >= 1, "empty row list");
     ATTNLAB_REQUIRE(rows == nullptr || rows_stride >= S, "rows_stride=%lld smaller than S=%d", (long long)rows_stride, S);
     ATTNLAB_REQUIRE(k == 0 || (scores != nullptr && score_stride >= M), "scores must hold M=%d values per row", M);
+    return ATTNLAB_OK;
+}
+
+int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
+                     int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                     void* scratch, int64_t scratch_bytes, hipStream_t stream) {
+    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride);
+    if (rc) return rc;
     ATTNLAB_REQUIRE(scratch_bytes >= 0, "negative scratch_bytes");
-    if (!rows && !rows_flat && !state) return ATTNLAB_OK;
+    const int M = hi - lo;
     const int R = B * G;
+    const bool staged = k > 0 && staged_score_order(order, k);
+    ATTNLAB_REQUIRE(!staged || (scratch != nullptr && (reinterpret_cast<uintptr_t>(scratch) & 255) == 0 &&
+                                scratch_bytes >= select_scratch_bytes(R, M, k, order)),
+                    "score order with k=%d > %d needs a 256-byte aligned scratch of attnlab_select_scratch_bytes = %lld "
+                    "bytes", k, kMaxScoreOrderK, (long long)select_scratch_bytes(R, M, k, order));
+    if (!rows && !rows_flat && !state) return ATTNLAB_OK;
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
     const int W = (M + 31) / 32;
     const bool tiled = state && scratch && k > 0 && W <= kMaxWords &&
-                       (reinterpret_cast<uintptr_t>(state) & 15) == 0 && (reinterpret_cast<uintptr_t>(scratch) & 3) == 0 &&
-                       scratch_bytes >= tiled_scratch_bytes(R, M);
-    if (!tiled) return launch_select(a, R, stream);
-    TiledArgs t;
-    t.above = static_cast<uint32_t*>(scratch);
-    t.cand = t.above + (size_t)R * W;
-    t.W = W;
-    t.T = (M + kTileKeys - 1) / kTileKeys;
-    return launch_tiled(a, t, R, stream);
+                       (reinterpret_cast<uintptr_t>(state) & 15) == 0 && (reinterpret_cast<uintptr_t>(scratch) & 15) == 0 &&
+                       scratch_bytes >= align_bytes(tiled_region_bytes(R, M), 256);
+    return run_select(a, R, tiled, scratch, stream, false);
 }
 
 }  // namespace attnlab
@@ -953,8 +1372,8 @@ extern "C" int attnlab_topk(const float* scores, int64_t score_stride, int R, in
     ATTNLAB_REQUIRE(R >= 0 && M >= 0, "R=%d and M=%d must be non-negative", R, M);
     ATTNLAB_REQUIRE(0 <= k && k <= M, "need 0 <= k <= M, got k=%d M=%d", k, M);
     ATTNLAB_REQUIRE(order == ATTNLAB_ORDER_POSITION || order == ATTNLAB_ORDER_SCORE, "unknown order %d", order);
-    ATTNLAB_REQUIRE(order != ATTNLAB_ORDER_SCORE || k <= kMaxScoreOrderK, "score order supports k <= %d, got %d",
-                    kMaxScoreOrderK, k);
+    ATTNLAB_REQUIRE(order != ATTNLAB_ORDER_SCORE || k <= kMaxScoreOrderK,
+                    "score order with k=%d > %d needs the scratch of attnlab_topk_tiled", k, kMaxScoreOrderK);
     if (R == 0 || k == 0) return ATTNLAB_OK;
     ATTNLAB_REQUIRE(scores != nullptr && score_stride >= M, "scores must hold M=%d values per row", M);
     ATTNLAB_REQUIRE(top_stride >= k, "top_stride=%lld smaller than k=%d", (long long)top_stride, k);
@@ -969,31 +1388,24 @@ extern "C" int attnlab_topk_tiled(const float* scores, int64_t score_stride, int
     ATTNLAB_REQUIRE(R >= 0 && M >= 0, "R=%d and M=%d must be non-negative", R, M);
     ATTNLAB_REQUIRE(0 <= k && k <= M, "need 0 <= k <= M, got k=%d M=%d", k, M);
     ATTNLAB_REQUIRE(order == ATTNLAB_ORDER_POSITION || order == ATTNLAB_ORDER_SCORE, "unknown order %d", order);
-    ATTNLAB_REQUIRE(order != ATTNLAB_ORDER_SCORE || k <= kMaxScoreOrderK, "score order supports k <= %d, got %d",
-                    kMaxScoreOrderK, k);
+    ATTNLAB_REQUIRE(scratch_bytes >= 0, "negative scratch_bytes");
     if (R == 0 || k == 0) return ATTNLAB_OK;
     ATTNLAB_REQUIRE(scores != nullptr && score_stride >= M, "scores must hold M=%d values per row", M);
     ATTNLAB_REQUIRE(top_stride >= k, "top_stride=%lld smaller than k=%d", (long long)top_stride, k);
-    const int W = (M + 31) / 32;
     ATTNLAB_REQUIRE(state != nullptr && (reinterpret_cast<uintptr_t>(state) & 15) == 0,
                     "state must be a 16-byte aligned [R, %d] buffer", kSelectStateWords);
-    ATTNLAB_REQUIRE(scratch != nullptr && (reinterpret_cast<uintptr_t>(scratch) & 3) == 0 &&
-                        scratch_bytes >= tiled_scratch_bytes(R, M),
-                    "scratch must hold attnlab_select_scratch_bytes(%d, %d) = %lld bytes", R, M,
-                    (long long)tiled_scratch_bytes(R, M));
+    const int64_t need = select_scratch_bytes(R, M, k, order);
+    ATTNLAB_REQUIRE(scratch != nullptr && (reinterpret_cast<uintptr_t>(scratch) & 255) == 0 && scratch_bytes >= need,
+                    "scratch must be 256-byte aligned and hold attnlab_select_scratch_bytes(%d, %d, %d, %d) = %lld bytes",
+                    R, M, k, order, (long long)need);
     SelectArgs a{scores, score_stride, M, k, 0, 0, 0, 1, 0, order, nullptr, 0, nullptr, top_idx, top_val, top_stride,
                  state};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (W > kMaxWords) {   // rows past 262144 keys: single-workgroup select, which builds its own histograms
+    if ((M + 31) / 32 > kMaxWords) {   // rows past 262144 keys: single-workgroup select, which builds its own histograms
         a.hist = nullptr;
-        return launch_select(a, R, s);
+        return run_select(a, R, false, scratch, s, false);
     }
-    TiledArgs t;
-    t.above = static_cast<uint32_t*>(scratch);
-    t.cand = t.above + (size_t)R * W;
-    t.W = W;
-    t.T = (M + kTileKeys - 1) / kTileKeys;
-    return launch_tiled(a, t, R, s, true);
+    return run_select(a, R, true, scratch, s, true);
 }
 
 extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal,
@@ -1003,7 +1415,7 @@ extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, in
                             scratch, scratch_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int64_t attnlab_select_scratch_bytes(int R, int M) {
-    if (R < 0 || M < 0) return -1;
-    return select_scratch_bytes(R, M);
+extern "C" int64_t attnlab_select_scratch_bytes(int R, int M, int k, int order) {
+    if (R < 0 || M < 0 || k < 0 || k > M) return -1;
+    return select_scratch_bytes(R, M, k, order);
 }

@@ -257,7 +257,7 @@ def launchers(ls, torch):
     # select state (top-k histograms and counters): zero once; each score/select pair leaves it zeroed
     step_hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
     hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
-    sel_bytes = lib.attnlab_select_scratch_bytes(B * G, ls.M)
+    sel_bytes = lib.attnlab_select_scratch_bytes(B * G, ls.M, ls.k, nat.ORDER_POSITION)
     sel_scratch = torch.empty(sel_bytes, dtype=torch.uint8, device=dev)
     u_buf = torch.zeros(B * G * r, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(d)
@@ -508,7 +508,7 @@ def sweep_lightning_topk(torch, dev, emit):
                 # the selection hip_select.topk runs for these rows: tiled over the chip for 8K..256K scores (state
                 # zeroed once, left zeroed by every call), one workgroup per row below
                 state = torch.zeros(B * KG, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
-                nbytes = nat.lib().attnlab_select_scratch_bytes(B * KG, L)
+                nbytes = nat.lib().attnlab_select_scratch_bytes(B * KG, L, k, nat.ORDER_SCORE)
                 scratch = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
                 tiled = hip_select.TILED_MIN_M <= L <= hip_select.TILED_MAX_M
 

@@ -32,7 +32,12 @@ extern "C" {
 /* Row-list order of attnlab_select_rows / attnlab_sparse_decode_step. */
 #define ATTNLAB_ORDER_POSITION 0 /* every row list ascending by position (canonical_order=True, decode.py:160-161) */
 #define ATTNLAB_ORDER_SCORE 1    /* F ascending, then the top-k by descending score, ties lowest index first
-                                    (cat(fixed_rows, topk.indices) of decode.py:86-93) */
+                                    (cat(fixed_rows, topk.indices) of decode.py:86-93); any k: up to
+                                    ATTNLAB_LDS_SORT_K pairs are sorted in LDS, more by a radix pass through the
+                                    select scratch */
+
+/* Largest k whose score order is sorted in one workgroup's LDS (attnlab_topk takes score order up to this k). */
+#define ATTNLAB_LDS_SORT_K 8192
 
 /* Index-key element types of the score kernels. */
 #define ATTNLAB_DT_BF16 0
@@ -150,7 +155,8 @@ int attnlab_score_lightning_batched(const uint16_t* keys, int key_dtype, const f
  * (row i at scores + i*score_stride) selects the k largest; equal scores resolve to the lower index; NaN ranks below
  * every number; -0.0 equals +0.0. Writes, when non-NULL, top_idx[i, 0..k) (int32 candidate-relative indices) and
  * top_val[i, 0..k) (the scores), row stride top_stride, in `order`: ATTNLAB_ORDER_POSITION (ascending index) or
- * ATTNLAB_ORDER_SCORE (descending score, then ascending index). Requires 0 <= k <= M.
+ * ATTNLAB_ORDER_SCORE (descending score, then ascending index). Requires 0 <= k <= M, and k <= ATTNLAB_LDS_SORT_K in
+ * score order (larger k: attnlab_topk_tiled, which has the scratch for the radix pass).
  */
 int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k, int order, int32_t* top_idx,
                  float* top_val, int64_t top_stride, void* stream);
@@ -158,9 +164,10 @@ int attnlab_topk(const float* scores, int64_t score_stride, int R, int M, int k,
 /*
  * attnlab_topk spread over the chip for long rows (the same selection, bit for bit): a histogram pass, a classify
  * pass over tiles of 4096 scores and one resolve workgroup per row, instead of one workgroup per row for every pass.
- * Replaces the same torch.topk call (decode.py:86-93). state: [R, ATTNLAB_SELECT_STATE_WORDS] uint32, 16-byte
- * aligned, zero on entry and left zero; scratch: at least attnlab_select_scratch_bytes(R, M) bytes, no
- * initialisation. Rows longer than 262144 scores run the single-workgroup select. Score order needs k <= 8192.
+ * Replaces the same torch.topk call (decode.py:86-93), for any k in either order. state: [R,
+ * ATTNLAB_SELECT_STATE_WORDS] uint32, 16-byte aligned, zero on entry and left zero; scratch: 256-byte aligned, at least
+ * attnlab_select_scratch_bytes(R, M, k, order) bytes, no initialisation. Rows longer than 262144 scores run the
+ * single-workgroup select.
  */
 int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, int k, int order, int32_t* top_idx,
                        float* top_val, int64_t top_stride, uint32_t* state, void* scratch, int64_t scratch_bytes,
@@ -173,20 +180,23 @@ int attnlab_topk_tiled(const float* scores, int64_t score_stride, int R, int M, 
  * scores: [B*G] rows of M = hi - lo candidate scores (row stride score_stride). F = [0, lo) U [hi, legal).
  * S = lo + (legal - hi) + k. rows: [B*G, S] int32 positions (row stride rows_stride; nullable). rows_flat: [B*G*S]
  * int64 flat row ids pos + (b*G+g)*C of the flattened [B*G*C, d] cache (sparse.py:14-16; nullable).
- * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE (the latter needs k <= 8192).
+ * order: ATTNLAB_ORDER_POSITION or ATTNLAB_ORDER_SCORE.
  * state (nullable): the select state [B*G, ATTNLAB_SELECT_STATE_WORDS] attnlab_score_grouped filled for these scores;
  * when given, the first radix pass is skipped and the state is left zeroed for the next call.
- * scratch (nullable, 4-byte aligned, no zeroing needed): with state, position order, 0 < k, hi - lo <= 262144 and
- * scratch_bytes >= attnlab_select_scratch_bytes(B*G, hi - lo), the keys are classified by a grid of 4096-key tiles
- * and each row resolved by one workgroup (two launches) instead of one workgroup per row reading every key three
- * times; the result is the same.
+ * scratch (256-byte aligned, no zeroing needed; nullable except in score order with k > ATTNLAB_LDS_SORT_K): with
+ * state, 0 < k, hi - lo <= 262144 and scratch_bytes >= attnlab_select_scratch_bytes(B*G, hi - lo, k, order), the keys
+ * are classified by a grid of 4096-key tiles and each row resolved by one workgroup (two launches) instead of one
+ * workgroup per row reading every key three times; the result is the same. Every argument check runs before the first
+ * launch.
  */
 int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
                         int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
                         void* scratch, int64_t scratch_bytes, void* stream);
 
-/* Scratch bytes of the tiled select of attnlab_select_rows for R rows of M candidates (-1 for negative sizes). */
-int64_t attnlab_select_scratch_bytes(int R, int M);
+/* Scratch bytes of attnlab_select_rows / attnlab_topk_tiled for R rows of M candidates and top-k in `order`: the
+ * tiled select's bitmaps and candidate entries, plus the radix pass's buffers in score order with
+ * k > ATTNLAB_LDS_SORT_K (-1 for negative sizes or k outside [0, M]). */
+int64_t attnlab_select_scratch_bytes(int R, int M, int k, int order);
 
 /*
  * Gather-free sparse attention. Replaces MetalAttend.__call__ (metal_attend.py:226-250, kernels :46-169) and the

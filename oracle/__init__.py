@@ -20,7 +20,8 @@ How each function is pinned (no function here is "parity unpinned"):
   rules      the known answers of the reference's tests (test_attention_contracts.py:309-347, 237-239, 262;
              test_qwen_wrapper.py:387-392) - tests/test_oracle_pins.py
   exact      closed forms that a dropped term / wrong index / transposed operand breaks (unit-vector queries pick one
-             table row, S=1 attention returns the V row, equal scores return the V mean, softmax invariance to a
+             table row, unit rows of wk make project_keys pick one key coordinate per index dim and its columns equal
+             z_column of each key, S=1 attention returns the V row, equal scores return the V mean, softmax invariance to a
              shift, k0 = capacity sparse == dense, score == the explicit double loop on tiny inputs), brute force
              (top-k against a full sort, including planted ties, NaN and -0.0), and cross-checks of the two
              independent formulations (masked dense vs listed subset; the masked prefill read vs one sliced dense

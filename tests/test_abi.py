@@ -61,16 +61,26 @@ def test_invalid_arguments_are_rejected_before_any_launch(native_lib):
                      None, 256, 10, None, None, 16, None)
 
 
-def select_scratch(R, M):
-    """Tiled select scratch: two bitmaps of one bit per candidate (keys above the threshold's first digit, keys
-    sharing it), in 32-bit words."""
-    return R * 2 * 4 * ((M + 31) // 32)
+def _a(x, n=256):
+    return (x + n - 1) // n * n
+
+
+def select_scratch(R, M, k, order):
+    """Select scratch. Rows of at most 8 tiles of 4096 keys: per row the above-threshold bitmap (16-byte aligned), 32
+    (above, candidate) count pairs and 32 x 128 candidate entries of 8 bytes; longer rows: two bitmaps of one bit per
+    candidate. Score order past k = 8192 adds the radix pass's stage (4 bytes) and two buffers (8 bytes) per pick."""
+    words = (M + 31) // 32
+    region = R * (_a(words * 4, 16) + 32 * 8 + 4096 * 8) if M <= 32768 else R * 2 * 4 * words
+    extra = _a(R * k * 4) + 2 * _a(R * k * 8) if (order == 1 and k > 8192) else 0
+    return _a(region) + extra
 
 
 def test_select_scratch_formula(native_lib):
-    for R, M in ((128, 32704), (8, 1), (1, 4096), (1, 4097), (3, 0)):
-        assert native_lib.attnlab_select_scratch_bytes(R, M) == select_scratch(R, M)
-    assert native_lib.attnlab_select_scratch_bytes(-1, 5) == -1
+    for R, M, k, order in ((128, 32704, 1024, 0), (8, 1, 1, 1), (1, 4096, 9000 // 3, 1), (1, 40000, 20000, 1),
+                           (2, 40000, 20000, 0), (3, 0, 0, 0), (4, 32768, 32768, 1), (16, 131072, 4096, 1)):
+        assert native_lib.attnlab_select_scratch_bytes(R, M, k, order) == select_scratch(R, M, k, order)
+    assert native_lib.attnlab_select_scratch_bytes(-1, 5, 1, 0) == -1
+    assert native_lib.attnlab_select_scratch_bytes(1, 5, 6, 0) == -1
 
 
 def test_workspace_size_formula(native_lib):
@@ -79,7 +89,7 @@ def test_workspace_size_formula(native_lib):
         BG, M, S = B * G, hi - lo, lo + (legal - hi) + k
         scores = a(BG * ((M + 3) // 4 * 4) * 4) if k > 0 else 0
         u = a(BG * 32 * 4) if k > 0 else 0
-        sel = a(select_scratch(BG, M)) if k > 0 else 0
+        sel = a(select_scratch(BG, M, k, 1)) if k > 0 else 0
         return scores + a(BG * S * 4) + u + sel + (a(BG * P * h * 130 * 4) if P > 1 else 0)
     for args in ((16, 8, 4, 4, 32704, 32768, 1024, 4), (1, 8, 2, 4, 1984, 2048, 64, 1), (2, 8, 2, 60, 60, 60, 0, 8)):
         assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)

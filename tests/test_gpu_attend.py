@@ -246,3 +246,33 @@ def test_full_attention_contract(gpu):
     p = np.exp(s - s.max(-1, keepdims=True))
     brute = np.einsum("bgic,bgcd->bgid", p / p.sum(-1, keepdims=True), f64(V4)[:, :, :L])
     assert float(np.abs(f64(out)[:, :, :, 0] - brute).max()) <= 2e-2
+
+
+@pytest.mark.parametrize("h,T,masked", [(2, 1, False), (2, 3, True), (4, 2, False), (8, 1, True)])
+def test_subset_attention_on_the_attend_kernel(gpu, h, T, masked):
+    """subset_attention (sparse.py:40-60) over an already gathered subset: the h*T query rows of a group share its S
+    rows; padded slots (valid_mask False) are not read, even when they hold NaN."""
+    from attention_lab.sparse import gather_rows, subset_attention
+    B, G, C, S = 2, 4, 600, 77
+    gen = torch.Generator().manual_seed(h * 10 + T)
+    K4 = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    V4 = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    q = torch.randn(B, G, h, T, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    sel = torch.stack([torch.randperm(C, generator=gen)[:S] for _ in range(B * G)]).view(B, G, S).to(gpu)
+    k_sub, v_sub = gather_rows(K4, sel), gather_rows(V4, sel)
+    valid = None
+    slots = np.broadcast_to(np.arange(S), (B, G, S)).copy()
+    if masked:
+        valid = torch.rand(B, G, S, generator=gen).to(gpu) > 0.3
+        k_sub[~valid] = float("nan")
+        v_sub[~valid] = float("nan")
+        slots = np.where(valid.cpu().numpy(), slots, -1)
+    out = subset_attention(q, k_sub, v_sub, valid)
+    torch.cuda.synchronize()
+    assert out.shape == (B, G, h, T, 128) and out.dtype == torch.bfloat16
+    qf = f64(q).reshape(B, G, h * T, 128)
+    want = exact.subset_attention(qf, f64(k_sub), f64(v_sub), slots).reshape(B, G, h, T, 128)
+    d = np.abs(f64(out) - want)
+    assert np.isfinite(d).all() and d.max() <= 2e-2 and d.mean() <= 2e-3
+    with pytest.raises(ValueError):
+        subset_attention(torch.zeros(B, G, 8, 2, 128, dtype=torch.bfloat16, device=gpu), k_sub, v_sub)   # h*T > 8

@@ -69,6 +69,8 @@ def check_out(out, ref, what):
     (1, 2, 300, 256, 1 / 8, False),             # (lo, hi, k) = (4, 192, 32)
     (1, 2, 200, 128, 1 / 8, True),              # (68, 16, 84)
     (3, 1, 1000, 1000, 1 / 32, False),
+    (1, 2, 32768 + 64, 32768, 1 / 2, False),    # score order past the LDS sort: k = 16384 (radix pass)
+    (1, 2, 32768, 32768, 1.0, False),           # every candidate, score order: k = M = 32700
 ])
 def test_step_matches_oracle(gpu, B, h, C, L, rho, canonical):
     K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L)
@@ -221,3 +223,54 @@ def test_graph_replay_matches_eager(gpu):
         assert torch.equal(captured, eager)
         dense_decode_step(q, K, V, L)                               # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_rejected_call_leaves_the_select_state_clean(gpu):
+    """A call the select rejects (an unknown row order) must fail before the score kernel adds its histogram into the
+    shared select state: the next valid call's rows are still bit-exact against the oracle."""
+    from attention_lab import _native as nat
+    from attention_lab import decode as dec
+    B, G, h, C, L = 1, 8, 2, 2048 + 64, 2048
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=31)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=1 / 32, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    run_step(gpu, K, V, q, q_pre, k_pre_new, zT.clone(), idx, L, 1 / 32, False)   # sizes the module workspace
+    ws = dec._STEP_WS.bytes(gpu, 0, "step")
+    state = dec._STEP_WS.bytes(gpu, 0, "state")
+    out = torch.empty(B, G, h, 128, dtype=torch.bfloat16, device=gpu)
+    qm = q.reshape(B, G, h, 128).contiguous()
+    qc = q_pre.reshape(B, G, h * 128).contiguous()
+    kn = k_pre_new.reshape(B, G, 128).contiguous()
+    with pytest.raises(ValueError, match="order"):
+        nat.call("attnlab_sparse_decode_step", qm.data_ptr(), qc.data_ptr(), K.data_ptr(), V.data_ptr(),
+                 zT.data_ptr(), idx.wq_t_scaled.data_ptr(), idx.wk.data_ptr(), kn.data_ptr(), B, G, h, 32, C, lo, hi,
+                 L, k, L - 1, 0.088, 7, 1, state.data_ptr(), ws.data_ptr(), ws.numel(), None, None, out.data_ptr(),
+                 nat.stream_of(gpu))
+    torch.cuda.synchronize()
+    assert int(state[:B * G * nat.SELECT_STATE_WORDS * 4].abs().sum()) == 0, "the rejected call touched the state"
+    for canonical in (False, True):
+        z = zT.clone()
+        _, out2, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, z, idx, L, 1 / 32, canonical)
+        s = kernel_scores(z, q_pre, idx, lo, hi)
+        want = exact.select_rows(s, lo, hi, L, k, order="position" if canonical else "score")
+        assert np.array_equal(pos, want), f"canonical={canonical}: rows differ after a rejected call"
+
+
+def test_a_fixed_set_other_than_the_rule_is_refused(gpu):
+    """The step writes F from (lo, hi, legal) where the reference concatenates the fixed_rows it is given: any other
+    set raises ValueError (select_rows_kernel and sparse_decode_step_kernel), an equal untagged copy is accepted."""
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=1, C=600, seed=12)
+    L = 512
+    req = prepare_request(1, 8, 600, valid_length=L, query_position=L - 1, rho=1 / 8, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    other = req.fixed_rows.clone()
+    other[0, 0, 0] = other[0, 0, 0] + 7                               # a candidate row in place of position 0
+    with pytest.raises(ValueError, match="selection rule"):
+        sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, other, req.off_lo, lo, hi, k, S)
+    with pytest.raises(ValueError, match="selection rule"):
+        select_rows_kernel(idx.query(q_pre), zT, other, req.off_lo, lo, hi, k)
+    a = sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo, lo, hi, k, S)
+    b = sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows.clone(),
+                                  req.off_lo.clone(), lo, hi, k, S)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -31,8 +31,6 @@ def check_topk(gpu, s: np.ndarray, k: int):
     """Both selections (one workgroup per row; histogram + classify + resolve over the chip) against the oracle."""
     t = torch.from_numpy(s).to(gpu)
     for order in ("score", "position"):
-        if order == "score" and k > hip_select.MAX_SCORE_ORDER_K:
-            continue
         want = exact.topk(s, k, order=order)
         for tiled in (False, True):
             vals, idx = hip_select.topk(t, k, order=order, tiled=tiled)
@@ -63,6 +61,19 @@ def test_topk_position_order_large_k(gpu, M, k):
 def test_score_order_beyond_4096(gpu, M, k):
     """Score order sorts up to 8192 selected pairs in LDS (both selections)."""
     check_topk(gpu, heavy_tail(2, M, seed=k), k)
+
+
+@pytest.mark.parametrize("M,k,gen", [(32700, 16384, "normal"), (40000, 20000, "normal"), (32768, 32768, "normal"),
+                                     (20000, 9000, "ties"), (12000, 10000, "specials"), (10000, 9000, "zeros"),
+                                     (300000, 9000, "normal")])
+def test_score_order_past_the_lds_sort(gpu, M, k, gen):
+    """Score order with k > 8192: the position-order select, then the stable radix pass; ties stay in index order,
+    NaN last, -0.0 == +0.0; the compact, bitmap and single-workgroup (M > 262144) selects all feed it."""
+    rng = np.random.default_rng(M + k)
+    R = 2
+    s = {"normal": lambda: heavy_tail(R, M, seed=k), "ties": lambda: tie_heavy(rng, (R, M)),
+         "specials": lambda: specials(rng, (R, M)), "zeros": lambda: np.zeros((R, M), np.float32)}[gen]()
+    check_topk(gpu, s, k)
 
 
 def test_ties_resolve_to_the_lowest_index(gpu):
@@ -98,7 +109,8 @@ def test_nan_signed_zero_and_infinities(gpu):
 
 @pytest.mark.parametrize("legal,k0,order", [(2048, 64, "position"), (2048, 64, "score"), (300, 37, "score"),
                                             (60, 10, "position"), (32768, 1024, "position"), (32768, 1024, "score"),
-                                            (100, 0, "score"), (1000, 932, "position")])
+                                            (100, 0, "score"), (1000, 932, "position"), (32768, 16384, "score"),
+                                            (32768, 32700, "score"), (20000, 9000, "score")])
 def test_select_rows_matches_oracle(gpu, legal, k0, order):
     from oracle import rules
     B, G = 2, 8
@@ -115,18 +127,22 @@ def test_select_rows_matches_oracle(gpu, legal, k0, order):
     assert np.array_equal(flat.cpu().numpy().reshape(B, G, S), want + off)
 
 
-@pytest.mark.parametrize("B,C,L,order,tiled", [(1, 2048 + 64, 2048, "position", True), (4, 32768, 32768, "score", True),
-                                               (2, 70000, 70000, "position", True), (3, 1000, 777, "score", True),
-                                               (2, 32768, 32768, "position", False),
-                                               (2, 140000, 140000, "position", True)])
-def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order, tiled):
+@pytest.mark.parametrize("B,C,L,order,tiled,rho", [(1, 2048 + 64, 2048, "position", True, 1 / 32),
+                                                   (4, 32768, 32768, "score", True, 1 / 32),
+                                                   (2, 70000, 70000, "position", True, 1 / 32),
+                                                   (3, 1000, 777, "score", True, 1 / 32),
+                                                   (2, 32768, 32768, "position", False, 1 / 32),
+                                                   (2, 140000, 140000, "position", True, 1 / 32),
+                                                   (2, 32768, 32768, "score", True, 1 / 2),
+                                                   (1, 40000, 40000, "score", True, 1 / 4)])
+def test_histogram_handoff_from_the_score_kernel(gpu, B, C, L, order, tiled, rho):
     """score_grouped(state=) + select_rows(state=) gives exactly the rows of the self-contained select, leaves the
     state zeroed, and stays exact over repeated calls on fresh data (a stale histogram would break it)."""
     from attention_lab import _native as nat
     from attention_lab import hip_score
     from oracle import rules
     G, r = 8, 32
-    lo, hi, k, S = rules.step(L, rules.budget(L, 1 / 32))
+    lo, hi, k, S = rules.step(L, rules.budget(L, rho))
     state = torch.zeros(B, G, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
     for rep in range(3):
         gen = torch.Generator().manual_seed(100 * rep + B)
@@ -275,8 +291,6 @@ def test_validation(gpu):
         hip_select.topk(t, 101)
     with pytest.raises(ValueError):
         hip_select.topk(t.double(), 3)
-    with pytest.raises(ValueError):
-        hip_select.topk(torch.zeros(2, 10000, device=gpu), 9000, order="score")
     with pytest.raises(ValueError):
         hip_select.topk(t, 3, order="random")
     with pytest.raises(ValueError):

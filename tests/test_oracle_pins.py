@@ -127,6 +127,36 @@ def test_z_column_closed_form():
     np.testing.assert_array_equal(bits, bf16.from_f32(z.astype(np.float32)))
 
 
+def test_project_keys_pins():
+    """exact.project_keys (indexer.py:15-17), the bulk index-table build both MFMA kernels are checked against: unit
+    rows of wk pick one coordinate of every key, one column equals the separately written z_column of that key, a
+    double loop over (g, j, t, e) agrees, and the table is laid out [B, G, r, T] (index dim before position)."""
+    B, G, T, r, d = 2, 3, 7, 5, 6
+    perm = np.array([[(j * 2 + g) % d for j in range(r)] for g in range(G)])
+    wk = np.zeros((G, r, d))
+    for g in range(G):
+        for j in range(r):
+            wk[g, j, perm[g, j]] = 1.0
+    k_pre = RNG.standard_normal((B, G, T, d))
+    zT = exact.project_keys(k_pre, wk)
+    assert zT.shape == (B, G, r, T)
+    for g in range(G):
+        for j in range(r):
+            np.testing.assert_array_equal(zT[:, g, j, :], k_pre[:, g, :, perm[g, j]])
+    wk = RNG.standard_normal((G, r, d))
+    zT = exact.project_keys(k_pre, wk)
+    for t in range(T):
+        z, _ = exact.z_column(k_pre[:, :, t, :], wk)
+        np.testing.assert_allclose(zT[..., t], z, rtol=1e-13, atol=1e-13)
+    loop = np.zeros((B, G, r, T))
+    for b in range(B):
+        for g in range(G):
+            for j in range(r):
+                for t in range(T):
+                    loop[b, g, j, t] = sum(wk[g, j, e] * k_pre[b, g, t, e] for e in range(d))
+    np.testing.assert_allclose(zT, loop, rtol=1e-12, atol=1e-12)
+
+
 def test_lightning_reduces_to_grouped_and_relu_clamps():
     B, KG, L, r = 2, 3, 50, 32
     keys = RNG.standard_normal((B, KG, L, r))
@@ -281,6 +311,19 @@ def test_planted_mistakes_are_caught():
     # 4. a softmax that drops the scale differs from the reference scale
     sub = exact.subset_attention(q, K, V, rows)
     assert np.abs(sub - exact.subset_attention(q, K, V, rows, scale=1.0)).max() > 1e-4
+
+    # 5. a bulk index-table build with its output axes transposed ([B, G, T, r]) or contracting the wrong weight axis
+    #    fails project_keys' unit-row check
+    Gk, rk, dk, Tk = 1, 3, 3, 4
+    wk = np.zeros((Gk, rk, dk))
+    wk[0, 0, 2] = wk[0, 1, 0] = wk[0, 2, 1] = 1.0
+    k_pre = RNG.standard_normal((1, Gk, Tk, dk))
+    want = np.stack([k_pre[0, 0, :, 2], k_pre[0, 0, :, 0], k_pre[0, 0, :, 1]])
+    np.testing.assert_array_equal(exact.project_keys(k_pre, wk)[0, 0], want)
+    transposed_out = np.einsum("gjd,bgtd->bgtj", wk, k_pre)
+    wrong_axis = np.einsum("gdj,bgtd->bgjt", wk, k_pre)
+    assert transposed_out[0, 0].shape != want.shape or not np.array_equal(transposed_out[0, 0], want)
+    assert not np.array_equal(wrong_axis[0, 0], want)
 
 
 def test_causal_attention_is_one_dense_read_per_query():

@@ -135,3 +135,23 @@ def test_make_cache_takes_the_model_geometry():
     assert c.slots == 56 and tuple(c.k[0].shape) == (3, 2, 56, 16)
     assert c.k[0].dtype == torch.float32 and tuple(c.z[1].shape) == (3, 2, 8, 56)
     assert c.bytes()["total_bytes"] == sum(t.numel() * t.element_size() for t in c.k + c.v + c.z)
+
+
+def test_fixed_set_check_accepts_the_rule_and_refuses_anything_else():
+    """The HIP step writes F from (lo, hi, legal): the rule's F (tagged by prepare_request, or equal by value) passes,
+    any other fixed_rows / off_lo raises ValueError instead of being silently replaced."""
+    import torch
+    from attention_lab.decode import check_standard_f, prepare_request
+    req = prepare_request(2, 3, 300, valid_length=256, query_position=255, rho=1 / 8, device="cpu")
+    lo, hi, legal = req.layout.candidate_lo, req.layout.candidate_hi, req.layout.legal_length
+    check_standard_f(req.fixed_rows, req.off_lo, lo, hi, legal, 300)                  # tagged: no device read
+    check_standard_f(req.fixed_rows.clone(), req.off_lo.clone(), lo, hi, legal, 300)  # untagged, equal by value
+    bad = req.fixed_rows.clone()
+    bad[0, 1, 5] += 1
+    with pytest.raises(ValueError, match="selection rule"):
+        check_standard_f(bad, req.off_lo, lo, hi, legal, 300)
+    with pytest.raises(ValueError, match="selection rule"):
+        check_standard_f(req.fixed_rows.clone(), req.off_lo.clone() + 1, lo, hi, legal, 300)
+    with pytest.raises(ValueError, match="selection rule"):                            # a different capacity
+        check_standard_f(req.fixed_rows.clone(), req.off_lo.clone(), lo, hi, legal, 301)
+    assert torch.equal(req.fixed_rows[1, 2], req.fixed_positions[1, 2] + (1 * 3 + 2) * 300)
