@@ -319,3 +319,34 @@ def test_native_runner_matches_the_unmodified_model_and_rolls_back():
         run.rollback(50)
         again = torch.cat([run.step(ids[:, i:i + 1]) for i in range(50, 60)], 1)
         assert_close(again, tail, TOL, "native replay after rollback")
+
+
+@pytest.mark.parametrize("canonical", [False, True])
+def test_every_candidate_at_32k_in_either_row_order_equals_the_full_read(gpu, canonical):
+    """k0 = capacity at a 32K context selects ~32.7K candidates per step: score order (the wrapper's default, its
+    radix pass) and position order must both read exactly the full legal range and match the full read (reference
+    tests/test_qwen_wrapper.py:150-173)."""
+    m, _ = tiny_pair(gpu, seed=11)
+    L = 32768
+    ids = token_ids(L + 3, seed=11).to(gpu)
+    with torch.inference_mode():
+        holder = wrap_model(m)
+        stA = make_state(m, L + 8, "full")
+        runA = LabRunner(m, holder, stA)
+        runA.prefill(ids[:, :L], 8192)
+        stD = make_state(m, L + 8, "sparse", canonical_order=canonical)
+        runD = LabRunner(m, holder, stD)
+        runD.prefill(ids[:, :L], 8192)
+        stD.begin_request(None, k0=stD.cache.capacity)
+        stD.record_selection = True
+        for i in range(L, L + 3):
+            a = runA.step(ids[:, i:i + 1])
+            d = runD.step(ids[:, i:i + 1])
+            plan = stD.plan
+            assert plan.k == plan.candidate_count > 8192 and plan.selected_count == plan.legal_length
+            rows = stD.last_rows[0].view(1, stD.cache.groups, plan.selected_count) - stD.cache.offsets
+            assert torch.equal(rows.sort(dim=-1).values[0, 0].cpu(), torch.arange(plan.legal_length))
+            if canonical:
+                assert torch.equal(rows[0, 0].cpu(), torch.arange(plan.legal_length))
+            assert_close(d, a, TOL, f"step {i}: every candidate ({'position' if canonical else 'score'} order) vs full")
+        unwrap_model(m)
