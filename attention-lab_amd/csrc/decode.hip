@@ -125,3 +125,87 @@ extern "C" int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const floa
                                                    C, 128, h * 128, slo, shi, write_col, st, s);
         });
 }
+
+// ---------------------------------------------------------------------------------------------------------------
+// attnlab_sparse_decode_step_noalloc: the bf16 step with its select state and workspace in a file-scope device array
+// instead of caller buffers, for callers that cannot allocate. The array's device address comes from
+// hipGetSymbolAddress once per device (the array's name is only a host-side stand-in); every call on a device shares
+// that device's copy, so calls that overlap on one device race. Layout: the select state of up to kNoAllocRows rows at
+// the start (it must read zero at the start of a call: it is cleared by a fill kernel on a device's first call and
+// after any failed call, and every completed call leaves the rows it used zeroed), then the step's workspace.
+// ---------------------------------------------------------------------------------------------------------------
+#include <mutex>
+
+namespace {
+
+constexpr int64_t kNoAllocBytes = 32ll << 20;   // 32 MiB per device, held until the process ends
+constexpr int kNoAllocRows = 256;                // B * G rows of select state
+constexpr int64_t kNoAllocStateBytes = (int64_t)kNoAllocRows * ATTNLAB_SELECT_STATE_WORDS * 4;
+constexpr int kNoAllocMaxDevices = 64;
+static_assert(kNoAllocStateBytes % kAlign == 0, "the workspace after the state stays 256-byte aligned");
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+struct NoAllocDevice {
+    char* ptr = nullptr;   // device address of `scratch` on this device
+    bool state_dirty = true;
+};
+std::mutex g_noalloc_mu;
+NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+
+__global__ __launch_bounds__(256) void noalloc_clear_state(uint4* p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+}  // namespace
+
+extern "C" int attnlab_sparse_decode_step_noalloc(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K,
+                                                  const uint16_t* V, uint16_t* zT, const uint16_t* wq_t,
+                                                  const uint16_t* wk, const uint16_t* k_new, int B, int G, int h, int r,
+                                                  int C, int lo, int hi, int legal, int k, int write_col, float scale,
+                                                  int order, int P, int32_t* rows_out, int64_t* rows_flat,
+                                                  uint16_t* out, void* stream) {
+    using namespace attnlab;
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && (int64_t)B * G <= kNoAllocRows, "B*G=%lld rows exceed the %d of the no-allocation "
+                    "entry point", (long long)B * G, kNoAllocRows);
+    const int64_t ws = attnlab_sparse_decode_workspace(B, G, h, lo, hi, legal, k, P);
+    ATTNLAB_REQUIRE(ws >= 0, "invalid sizes B=%d G=%d h=%d lo=%d hi=%d legal=%d k=%d P=%d", B, G, h, lo, hi, legal, k, P);
+    ATTNLAB_REQUIRE(kNoAllocStateBytes + ws <= kNoAllocBytes, "this step needs %lld bytes of workspace; the no-allocation "
+                    "entry point holds %lld", (long long)ws, (long long)(kNoAllocBytes - kNoAllocStateBytes));
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(ATTNLAB_ERUNTIME, "hipGetDevice: %s", hipGetErrorString(e));
+    ATTNLAB_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, "device %d outside the %d the library tracks", dev,
+                    kNoAllocMaxDevices);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    char* base;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        NoAllocDevice& d = g_noalloc[dev];
+        if (d.ptr == nullptr) {
+            void* p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr)
+                return set_error(ATTNLAB_ERUNTIME, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            d.ptr = static_cast<char*>(p);
+        }
+        if (d.state_dirty) {
+            hipLaunchKernelGGL(noalloc_clear_state, dim3(512), dim3(256), 0, s, reinterpret_cast<uint4*>(d.ptr),
+                               kNoAllocStateBytes / 16);
+            const int rc = check_launch("noalloc_clear_state");
+            if (rc) return rc;
+            d.state_dirty = false;
+        }
+        base = d.ptr;
+    }
+    const int rc = attnlab_sparse_decode_step(q_main, q_cat, K, V, zT, wq_t, wk, k_new, B, G, h, r, C, lo, hi, legal, k,
+                                              write_col, scale, order, P, reinterpret_cast<uint32_t*>(base),
+                                              base + kNoAllocStateBytes, kNoAllocBytes - kNoAllocStateBytes, rows_out,
+                                              rows_flat, out, stream);
+    if (rc != ATTNLAB_OK) {   // a launch may have run before the failure: clear the state before the next call
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        g_noalloc[dev].state_dirty = true;
+    }
+    return rc;
+}

@@ -273,6 +273,21 @@ int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const float* q_cat, c
                                    int order, int P, uint32_t* state, void* workspace, int64_t workspace_bytes,
                                    int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream);
 
+/*
+ * attnlab_sparse_decode_step with no allocation and no caller buffers beyond its inputs and outputs. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The select state and the workspace live in a 32 MiB file-scope device array
+ * that each device holds until the process ends; its first 256 * ATTNLAB_SELECT_STATE_WORDS words are the select state
+ * (B*G <= 256), the rest the workspace (attnlab_sparse_decode_workspace of these sizes must fit, or the call returns
+ * ATTNLAB_EINVAL). Arguments and outputs as in attnlab_sparse_decode_step (bf16 index table). Every call on a device
+ * shares that device's array: calls that overlap on one device race, so order them on one stream.
+ */
+int attnlab_sparse_decode_step_noalloc(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K,
+                                       const uint16_t* V, uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk,
+                                       const uint16_t* k_new, int B, int G, int h, int r, int C, int lo, int hi,
+                                       int legal, int k, int write_col, float scale, int order, int P,
+                                       int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
