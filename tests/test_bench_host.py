@@ -110,3 +110,21 @@ def test_p0_p1_geometry_matches_the_reference_benches():
     assert lay.fixed_count + k == 1076 and k == 1008
     L, C, lay, k = bench.p_geometry(8192, 1 / 32)
     assert lay.fixed_count + k == 324 and k == 256
+
+
+def test_cpu_info_and_the_lightning_cpu_leg():
+    """The CPU baseline's host facts (the CPUs the all-cores leg uses never exceed what the process may run on) and
+    its configs[1] leg, which must compute the lightning score + top-k the oracle defines."""
+    import numpy as np
+    import torch
+
+    import bench
+    from oracle import exact
+    info = bench.cpu_info()
+    assert 1 <= info["usable_cpus"] <= info["affinity_cpus"] <= info["logical_cpus"]
+    g = torch.Generator().manual_seed(3)
+    keys, q, w = torch.randn(8, 500, 32, generator=g), torch.randn(8, 4, 32, generator=g), torch.rand(8, 4, generator=g)
+    vals, idx = bench._lightning_cpu(torch, keys, q, w, 16)
+    s = exact.lightning_scores(keys.double().numpy()[None], q.double().numpy()[None], w.double().numpy()[None], 0, 500)[0]
+    np.testing.assert_allclose(vals.numpy(), np.take_along_axis(s, idx.numpy(), -1), rtol=1e-5, atol=1e-5)
+    assert np.array_equal(np.sort(idx.numpy(), -1), np.sort(exact.topk(s.astype(np.float32), 16), -1))
