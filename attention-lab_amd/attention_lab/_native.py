@@ -45,6 +45,7 @@ SIGNATURES = {
     "attnlab_select_scratch_bytes": (_i64, [_i] * 4),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
+    "attnlab_attend_paged": (_i, [_p, _p, _i, _i, _p, _i64, _i, _p, _p, _i64] + [_i] * 5 + [_f, _p, _i, _p, _p]),
     "attnlab_prefill_attend": (_i, [_p, _p, _p, _i64, _i, _p] + [_i] * 8 + [_f, _p]),
     "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
     "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),

@@ -213,6 +213,73 @@ def attend(q, k, v, rows, *, scale=None, partitions=None, out=None, out_dtype=to
     return out
 
 
+def attend_paged(q, k_pages, v_pages, block_table, rows=None, *, length=None, scale=None, partitions=None, out=None,
+                 out_dtype=torch.bfloat16, workspace=None):
+    """Gather-free attention over a paged cache: q [B,G,h,d]; k_pages / v_pages [num_pages, G, page_size, d] bf16 pools;
+    block_table int32 [B, max_pages] (the pool page of each sequence's logical page); rows int32 [B,G,S] positions, or
+    None with `length` for the dense read of positions [0, length). -> out [B,G,h,d]. Listed positions on a page entry
+    outside [0, num_pages) (e.g. -1 for unmapped) are skipped."""
+    if q.dim() != 4 or q.dtype != torch.bfloat16 or not q.is_contiguous() or q.shape[3] != HEAD_DIM:
+        raise ValueError("q must be a contiguous bfloat16 [B, G, h, 128] tensor")
+    B, G, h, _ = q.shape
+    if not 1 <= h <= MAX_H:
+        raise ValueError(f"h must be in [1, {MAX_H}]")
+    if (k_pages.dim() != 4 or k_pages.dtype != torch.bfloat16 or not k_pages.is_contiguous() or k_pages.shape[1] != G
+            or k_pages.shape[3] != HEAD_DIM or v_pages.shape != k_pages.shape or v_pages.dtype != torch.bfloat16
+            or not v_pages.is_contiguous()):
+        raise ValueError("k_pages / v_pages must be contiguous bfloat16 [num_pages, G, page_size, 128] pools")
+    num_pages, page = int(k_pages.shape[0]), int(k_pages.shape[2])
+    if page & (page - 1):
+        raise ValueError("page_size must be a power of two")
+    if (block_table.dim() != 2 or block_table.shape[0] != B or block_table.dtype != torch.int32
+            or block_table.stride(1) != 1):
+        raise ValueError("block_table must be an int32 [B, max_pages] tensor with unit column stride")
+    max_pages = int(block_table.shape[1])
+    for t in (k_pages, v_pages, block_table):
+        if t.device != q.device:
+            raise ValueError("all inputs must live on one device")
+    if rows is None:
+        if length is None or not 1 <= int(length) <= max_pages * page:
+            raise ValueError("without rows, length must be in [1, max_pages * page_size]")
+        S, rows_ptr, rows_stride = int(length), None, 0
+    else:
+        if rows.dim() != 3 or tuple(rows.shape[:2]) != (B, G) or rows.dtype != torch.int32 or not rows.is_contiguous():
+            raise ValueError("rows must be a contiguous int32 [B, G, S] tensor")
+        S, rows_ptr, rows_stride = int(rows.shape[2]), rows.data_ptr(), int(rows.shape[2])
+        if S < 1:
+            raise ValueError("at least one row must be selected")
+    P = sparse_partitions(B * G, S, h) if partitions is None else int(partitions)
+    if not 1 <= P <= MAX_P:
+        raise ValueError(f"partitions must be in [1, {MAX_P}]")
+    ws = _SHARED_WS if workspace is None else workspace
+    out = _out(out, (B, G, h, HEAD_DIM), out_dtype, q.device)
+    part = ws.bytes(q.device, B * G * P * h * (HEAD_DIM + 2) * 4, "attend_part") if P > 1 else None
+    sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    nat.call("attnlab_attend_paged", k_pages.data_ptr(), v_pages.data_ptr(), num_pages, page, block_table.data_ptr(),
+             block_table.stride(0), max_pages, q.data_ptr(), rows_ptr, rows_stride, B, G, h, S, P, sc, out.data_ptr(),
+             int(out.dtype == torch.bfloat16), nat.ptr(part), nat.stream_of(q.device))
+    return out
+
+
+def page_cache(k, v, page_size: int, *, spare_pages: int = 0, generator=None, fill=float("nan")):
+    """Copy a contiguous cache k, v [B,G,C,d] into pools of pages [B*ceil(C/page)+spare, G, page, d] placed in a
+    random order, with the block table [B, ceil(C/page)] int32 that finds them; unused pool pages hold `fill`. A
+    layout helper for tests and benches (one copy of the cache)."""
+    B, G, C, d = k.shape
+    npg = -(-C // page_size)
+    num = B * npg + int(spare_pages)
+    perm = torch.randperm(num, generator=generator)[:B * npg].view(B, npg).to(torch.int32)
+    kp = torch.full((num, G, page_size, d), fill, dtype=k.dtype, device=k.device)
+    vp = torch.full_like(kp, fill)
+    pad = npg * page_size - C
+    kk = torch.nn.functional.pad(k, (0, 0, 0, pad)) if pad else k
+    vv = torch.nn.functional.pad(v, (0, 0, 0, pad)) if pad else v
+    idx = perm.to(k.device).long()
+    kp[idx.reshape(-1)] = kk.view(B, G, npg, page_size, d).permute(0, 2, 1, 3, 4).reshape(B * npg, G, page_size, d)
+    vp[idx.reshape(-1)] = vv.view(B, G, npg, page_size, d).permute(0, 2, 1, 3, 4).reshape(B * npg, G, page_size, d)
+    return kp, vp, perm.to(k.device)
+
+
 def dense_decode(q, k, v, valid_length: int, *, scale=None, partitions=None, out=None, out_dtype=torch.bfloat16,
                  workspace=None):
     """Dense decode read A over positions [0, valid_length): q [B,G,h,d], k/v [B,G,C,d] -> out [B,G,h,d]."""

@@ -44,6 +44,12 @@ struct AttendArgs {
     void* out;
     int out_bf16;
     float* part;  // [BG, P, h, 130]: m, l, acc[128]
+    // paged layout (attend_kernel<..., PAGED = true>): K and V are pools of pages [pages, G, page, 128]; position p of
+    // (b, g) lives in row (block_table[b][p >> page_shift] * G + g) * page + (p & (page - 1)) of the pool. rows may be
+    // null there: the positions are then [0, S).
+    const int32_t* block_table = nullptr;
+    int64_t bt_stride = 0;
+    int G = 1, page_shift = 0, num_pages = 0;
 };
 
 __device__ __forceinline__ void merge_state(float& m, float& l, float& m2, float& l2, float& w1, float& w2) {
@@ -65,8 +71,9 @@ struct KVStage {
     bool ok;   // the entry exists and its position is inside [0, C)
 };
 
-template <int H, int D, bool DENSE>
+template <int H, int D, bool DENSE, bool PAGED = false>
 __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
+    static_assert(!(DENSE && PAGED), "the paged read lists its positions (rows, or [0, S) when rows is null)");
     constexpr int kChunk = 4096;   // row-list entries whose positions are staged in LDS at a time (one chunk for k <= 4096)
     __shared__ __attribute__((aligned(16))) int idx_sh[DENSE ? 4 : kChunk];
     __shared__ float red_ml[kMergeSlots][H][2];
@@ -100,9 +107,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
     const int Sp = (a.S + a.P - 1) / a.P;
     const int s_begin = p * Sp;
     const int s_end = min(a.S, s_begin + Sp);
-    const uint16_t* Kb = a.K + (size_t)bg * a.kv_bg_stride + 8 * sub;
-    const uint16_t* Vb = a.V + (size_t)bg * a.kv_bg_stride + 8 * sub;
-    const int32_t* rl = DENSE ? nullptr : a.rows + (size_t)bg * a.rows_stride;
+    const size_t bg_off = PAGED ? 0 : (size_t)bg * a.kv_bg_stride;   // a paged row index already names its (b, g)
+    const uint16_t* Kb = a.K + bg_off + 8 * sub;
+    const uint16_t* Vb = a.V + bg_off + 8 * sub;
+    const int32_t* rl = (DENSE || a.rows == nullptr) ? nullptr : a.rows + (size_t)bg * a.rows_stride;
 
     float m[H], l[H], acc[H][16];
 #pragma unroll
@@ -118,14 +126,36 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         const int clen = min(chunk, s_end - c0);
         if (!DENSE) {
             if (c0 != s_begin) __syncthreads();   // every wave is done with the previous chunk's positions
-            const int32_t* src = rl + c0;
-            if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {   // 16-byte loads where the chunk is aligned
-                const int nv = clen >> 2;
-                for (int i = tid; i < nv; i += kAttThreads)
-                    reinterpret_cast<int4*>(idx_sh)[i] = reinterpret_cast<const int4*>(src)[i];
-                for (int i = 4 * nv + tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+            if (PAGED && rl == nullptr) {
+                for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = c0 + i;
             } else {
-                for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+                const int32_t* src = rl + c0;
+                if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {   // 16-byte loads where the chunk is aligned
+                    const int nv = clen >> 2;
+                    for (int i = tid; i < nv; i += kAttThreads)
+                        reinterpret_cast<int4*>(idx_sh)[i] = reinterpret_cast<const int4*>(src)[i];
+                    for (int i = 4 * nv + tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+                } else {
+                    for (int i = tid; i < clen; i += kAttThreads) idx_sh[i] = src[i];
+                }
+            }
+            if (PAGED) {
+                // the staged positions become pool rows (-1: outside [0, C) or an unmapped page, never read); the
+                // 16-byte staging wrote each thread's four entries, the translation reads every 256th, hence the barrier
+                __syncthreads();
+                const int b = bg / a.G, g = bg - b * a.G;
+                const int32_t* bt = a.block_table + (size_t)b * a.bt_stride;
+                const int pmask = (1 << a.page_shift) - 1;
+                for (int i = tid; i < clen; i += kAttThreads) {
+                    const int pos = idx_sh[i];
+                    int prow = -1;
+                    if ((unsigned)pos < (unsigned)a.C) {
+                        const int page = bt[pos >> a.page_shift];
+                        if ((unsigned)page < (unsigned)a.num_pages)
+                            prow = ((page * a.G + g) << a.page_shift) + (pos & pmask);
+                    }
+                    idx_sh[i] = prow;
+                }
             }
             __syncthreads();
         }
@@ -139,7 +169,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         auto issue = [&](int j, KVStage& s) {
             const int e = (wave + kAttWaves * j) * 8 + slot;
             int pos = DENSE ? c0 + e : idx_sh[min(e, clen - 1)];
-            const bool ok = e < clen && (DENSE || (unsigned)pos < (unsigned)a.C);
+            const bool ok = e < clen && (DENSE || (PAGED ? pos >= 0 : (unsigned)pos < (unsigned)a.C));
             pos = ok ? pos : 0;
             const size_t off = (size_t)pos * a.kv_row_stride;
             s.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(Kb + off));
@@ -317,16 +347,16 @@ static int head_groups(int BG, int h, int P) {
     return Q;
 }
 
-template <bool DENSE>
+template <bool DENSE, bool PAGED = false>
 static int launch_attend(const AttendArgs& a, int BG, hipStream_t s) {
     const dim3 grid(BG * a.Q * a.P), block(kAttThreads);
     const int hq = a.h / a.Q;
-    if (hq <= 1) hipLaunchKernelGGL((attend_kernel<1, kStages, DENSE>), grid, block, 0, s, a);
-    else if (hq <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE>), grid, block, 0, s, a);
-    else if (hq <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attend_kernel<8, kStages, DENSE>), grid, block, 0, s, a);
+    if (hq <= 1) hipLaunchKernelGGL((attend_kernel<1, kStages, DENSE, PAGED>), grid, block, 0, s, a);
+    else if (hq <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE, PAGED>), grid, block, 0, s, a);
+    else if (hq <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE, PAGED>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attend_kernel<8, kStages, DENSE, PAGED>), grid, block, 0, s, a);
     if (a.P > 1) hipLaunchKernelGGL(attend_combine, dim3(BG), dim3(a.h * kHeadDim), 0, s, a);
-    return check_launch(DENSE ? "dense_decode" : "attend");
+    return check_launch(PAGED ? "attend_paged" : (DENSE ? "dense_decode" : "attend"));
 }
 
 static int check_common(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
@@ -370,4 +400,33 @@ extern "C" int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_
     AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, nullptr, 0, L, C, h, P, head_groups(B * G, h, P),
                  scale * kLog2e, out, out_bf16, part};
     return launch_attend<true>(a, B * G, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int attnlab_attend_paged(const uint16_t* K_pages, const uint16_t* V_pages, int num_pages, int page_size,
+                                    const int32_t* block_table, int64_t bt_stride, int max_pages, const uint16_t* q,
+                                    const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int P,
+                                    float scale, void* out, int out_bf16, float* part, void* stream) {
+    ATTNLAB_REQUIRE(page_size >= 1 && page_size <= (1 << 16) && (page_size & (page_size - 1)) == 0,
+                    "page_size=%d must be a power of two in [1, 65536]", page_size);
+    ATTNLAB_REQUIRE(num_pages >= 1 && max_pages >= 1, "num_pages=%d and max_pages=%d must be positive", num_pages,
+                    max_pages);
+    ATTNLAB_REQUIRE((int64_t)max_pages * page_size <= INT32_MAX, "max_pages * page_size exceeds 2^31 positions");
+    const int C = max_pages * page_size;   // logical capacity of one sequence
+    const int rc = check_common(K_pages, V_pages, (int64_t)C * kHeadDim, kHeadDim, q, B, G, h, C, P, out, part);
+    if (rc) return rc;
+    ATTNLAB_REQUIRE((int64_t)num_pages * G * page_size <= INT32_MAX, "the pool of %d pages x %d groups x %d rows "
+                    "exceeds 2^31 rows", num_pages, G, page_size);
+    ATTNLAB_REQUIRE(block_table != nullptr && bt_stride >= max_pages, "block_table must hold max_pages=%d entries per "
+                    "sequence", max_pages);
+    ATTNLAB_REQUIRE(S >= 1, "at least one row must be selected (S=%d)", S);
+    ATTNLAB_REQUIRE(rows == nullptr ? S <= C : rows_stride >= S, "rows must hold S=%d positions per (b, g) (or be "
+                    "null with S <= max_pages * page_size)", S);
+    AttendArgs a{K_pages, V_pages, 0, kHeadDim, q, rows, rows_stride, S, C, h, P, head_groups(B * G, h, P),
+                 scale * kLog2e, out, out_bf16, part};
+    a.block_table = block_table;
+    a.bt_stride = bt_stride;
+    a.G = G;
+    a.num_pages = num_pages;
+    while ((1 << a.page_shift) < page_size) ++a.page_shift;
+    return launch_attend<false, true>(a, B * G, reinterpret_cast<hipStream_t>(stream));
 }

@@ -223,6 +223,21 @@ int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_t kv_bg_str
                          int out_bf16, float* part, void* stream);
 
 /*
+ * attnlab_attend over a paged K/V cache (the layout option of the attend, metal_attend.py:226-235; no reference
+ * kernel reads pages). K_pages, V_pages: pools [num_pages, G, page_size, 128] bf16 shared by all sequences;
+ * block_table: int32 [B, bt_stride], entry j of sequence b = the pool page holding its positions
+ * [j * page_size, (j + 1) * page_size) for all G groups (j < max_pages). Position p of (b, g) is read from pool row
+ * (block_table[b][p / page_size] * G + g) * page_size + p % page_size. rows as in attnlab_attend (positions, row
+ * stride rows_stride), or NULL for the positions [0, S) (the dense read of a paged cache); listed positions outside
+ * [0, max_pages * page_size) or on a page entry outside [0, num_pages) are skipped, never read. page_size a power of
+ * two up to 65536; the pool at most 2^31 rows. q, out, P, part, scale as in attnlab_attend.
+ */
+int attnlab_attend_paged(const uint16_t* K_pages, const uint16_t* V_pages, int num_pages, int page_size,
+                         const int32_t* block_table, int64_t bt_stride, int max_pages, const uint16_t* q,
+                         const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int P, float scale,
+                         void* out, int out_bf16, float* part, void* stream);
+
+/*
  * Causal prefill read on the matrix cores: full_attention (full.py:17-44) for a chunk of T > 1 queries, with the
  * reference's legality rule (reference.py:41-48). Query t sits at position q_pos0 + t and reads the cache rows
  * j <= q_pos0 + t, j < legal:

@@ -276,3 +276,44 @@ def test_subset_attention_on_the_attend_kernel(gpu, h, T, masked):
     assert np.isfinite(d).all() and d.max() <= 2e-2 and d.mean() <= 2e-3
     with pytest.raises(ValueError):
         subset_attention(torch.zeros(B, G, 8, 2, 128, dtype=torch.bfloat16, device=gpu), k_sub, v_sub)   # h*T > 8
+
+
+@pytest.mark.parametrize("page,P,B,h", [(16, 1, 2, 2), (16, 8, 1, 4), (1, 4, 1, 2), (256, 2, 3, 1), (64, 16, 2, 8)])
+def test_paged_cache_reads_exactly_what_the_contiguous_cache_reads(gpu, page, P, B, h):
+    """The paged layout: pools of pages in a random order, unused pages NaN-poisoned, a block table per sequence.
+    Over the same row lists the paged read equals the contiguous one bit for bit (same arithmetic, other addresses) and
+    the float64 oracle within the bf16 bar; positions on an unmapped page (-1) are skipped."""
+    G, C, L = 8, 2300, 2200
+    K4, V4, q5 = make(gpu, G=G, h=h, C=C, seed=page + P, B=B)
+    q = q5[:, :, :, 0].contiguous()
+    rows = row_list(G, C, L, 1 / 16, seed=page, B=B)[0].to(torch.int32).to(gpu).contiguous()
+    gen = torch.Generator().manual_seed(page)
+    kp, vp, bt = hip_attend.page_cache(K4, V4, page, spare_pages=5, generator=gen)
+    flat = hip_attend.attend(q, K4, V4, rows, partitions=P, out_dtype=torch.float32)
+    paged = hip_attend.attend_paged(q, kp, vp, bt, rows, partitions=P, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(paged, flat), "paged and contiguous reads differ"
+    ref = exact.subset_attention(f64(q), f64(K4), f64(V4), rows.cpu().numpy())
+    assert np.abs(paged.double().cpu().numpy() - ref).max() <= TOL["out_atol"]
+    # unmapped pages: drop the last logical page of every sequence from the table; its listed positions are skipped
+    bt2 = bt.clone()
+    last = (L - 1) // page
+    bt2[:, last] = -1
+    dropped = torch.where(rows // page == last, torch.full_like(rows, -1), rows)
+    got = hip_attend.attend_paged(q, kp, vp, bt2, rows, partitions=P, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref2 = exact.subset_attention(f64(q), f64(K4), f64(V4), dropped.cpu().numpy())
+    assert torch.isfinite(got).all() and np.abs(got.double().cpu().numpy() - ref2).max() <= TOL["out_atol"]
+
+
+@pytest.mark.parametrize("page,L", [(16, 2048), (128, 1000)])
+def test_dense_read_of_a_paged_cache(gpu, page, L):
+    """rows=None reads positions [0, L) of each sequence through its block table: the dense control over pages."""
+    G, C, B, h = 8, 2048, 2, 2
+    K4, V4, q5 = make(gpu, G=G, h=h, C=C, seed=L, B=B)
+    q = q5[:, :, :, 0].contiguous()
+    kp, vp, bt = hip_attend.page_cache(K4, V4, page, generator=torch.Generator().manual_seed(L))
+    got = hip_attend.attend_paged(q, kp, vp, bt, None, length=L, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = exact.dense_attention(f64(q), f64(K4), f64(V4), L)
+    assert np.abs(got.double().cpu().numpy() - ref).max() <= TOL["out_atol"]
