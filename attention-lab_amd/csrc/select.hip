@@ -976,12 +976,12 @@ __global__ __launch_bounds__(kTileThreads) void select_classify_compact(SelectAr
     const int region = tile * kCompactWaves + wave;
     uint2* ent = t.entries + ((size_t)row * kCompactRegions + region) * kCompactWaveCap;
     uint32_t slot = (inc & 0xffffu) - nc;
-    uint32_t bits = cbits;
-    while (bits) {
-        const int i = __ffs(bits) - 1;
-        bits &= bits - 1;
-        if (slot < (uint32_t)kCompactWaveCap) ent[slot] = make_uint2((uint32_t)(i0 + i), low[i]);
-        ++slot;
+#pragma unroll
+    for (int i = 0; i < kTileKPT; ++i) {   // static indices: low[] stays in registers
+        if ((cbits >> i) & 1u) {
+            if (slot < (uint32_t)kCompactWaveCap) ent[slot] = make_uint2((uint32_t)(i0 + i), low[i]);
+            ++slot;
+        }
     }
     if (lane == 0) t.counts[(size_t)row * kCompactRegions + region] = make_uint2(tot >> 16, tot & 0xffffu);
 }

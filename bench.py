@@ -62,9 +62,13 @@ def parse_args():
     ap.add_argument("--no-b1", action="store_true", help="skip the batch-1 per-layer figures")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched (prefill) lightning score figure")
     ap.add_argument("--kernel-reps", type=int, default=20, help="graph replays per kernel-average measurement")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="short run for rocprofv3 --pmc passes: 5 scan launches of one layer at the bench shape, then "
-                         "5 plain 256 MiB device copies that calibrate the counters; prints one JSON line")
+    ap.add_argument("--pmc-workload", nargs="?", const="scan", choices=("scan", "select"),
+                    help="short run for rocprofv3 --pmc passes at the bench shape: 5 launches of one layer's scan "
+                         "(scan) or of its score + tiled select pair (select), then 5 plain 256 MiB device copies that "
+                         "calibrate the counters; prints one JSON line")
+    ap.add_argument("--pmc-table", nargs="+", metavar="DIR",
+                    help="per-kernel means of every counter in the rocprofv3 --pmc output directories given (FETCH_SIZE "
+                         "and WRITE_SIZE also in bytes, scaled by the 256 MiB calibration copy); no GPU needed")
     ap.add_argument("--sweeps", nargs="?", const="all", choices=("all", "score", "attend"),
                     help="instead of the bench line: the microbenchmark sweeps of BASELINE configs[1] (lightning score "
                          "+ top-k) and configs[2] (gather-free attend vs dense), one JSON line per case")
@@ -123,13 +127,18 @@ def pmc_workload(torch, dev, args):
                     layers=1, r=args.index_dim, rho=args.rho, seed=args.seed)
     fns = launchers(ls, torch)
     for _ in range(5):
-        fns["score"](0)
+        if args.pmc_workload == "select":
+            fns["score_select"](0)
+        else:
+            fns["score"](0)
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_workload": f"{SCAN_KERNEL} x5 then 256 MiB copy x5", "scan_algorithmic_bytes": ls.score_bytes(),
+    print(json.dumps({"pmc_workload": f"{'score + select' if args.pmc_workload == 'select' else SCAN_KERNEL} x5 then "
+                                      f"256 MiB copy x5", "select_algorithmic_bytes": ls.select_bytes(),
+                      "scores_bytes": ls.B * ls.G * 4 * ls.M, "scan_algorithmic_bytes": ls.score_bytes(),
                       "scan_read_bytes": ls.score_bytes() - ls.B * ls.G * (4 * ls.M + 2 * ls.r),
                       "scan_write_bytes": ls.B * ls.G * (4 * ls.M + 2 * ls.r),
                       "copy_bytes_each_way": PMC_COPY_BYTES}))
@@ -174,6 +183,38 @@ def pmc_summary(fetch_dir, write_dir):
            "dispatches": {"fetch": nf, "write": nw}, "traffic_read_bytes": read_b, "traffic_write_bytes": write_b,
            "traffic_bytes_per_launch": read_b + write_b}
     print(json.dumps(out, indent=1))
+    return 0
+
+
+def pmc_table(dirs):
+    """Mean value per dispatch of every counter, per kernel (names shortened), over the counter_collection.csv files of
+    the given rocprofv3 --pmc directories; FETCH_SIZE / WRITE_SIZE also as bytes, scaled by the 256 MiB copy."""
+    import csv
+    import glob
+    import re
+    sums: dict = {}
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path, newline="") as f:
+                for row in csv.DictReader(f):
+                    name = row.get("Kernel_Name", "")
+                    short = re.sub(r"^void |\(.*$|<.*$|attnlab::", "", name)
+                    key = (short, row["Counter_Name"])
+                    sums.setdefault(key, []).append(float(row["Counter_Value"]))
+    copy = {c: max(v) for (k, c), v in sums.items() if "copyBuffer" in k}
+    table: dict = {}
+    for (k, c), v in sorted(sums.items()):
+        if "copyBuffer" in k:
+            continue
+        if len(v) < 5:   # the workload's kernels run 5 times; torch's set-up kernels fewer
+            continue
+        mean = sum(v) / len(v)
+        ent = table.setdefault(k, {})
+        ent[c] = mean
+        if c in copy and c in ("FETCH_SIZE", "WRITE_SIZE"):
+            ent[c + "_bytes"] = mean * PMC_COPY_BYTES / copy[c]
+        ent["dispatches_" + c] = len(v)
+    print(json.dumps({"kernels": table, "copy_reading": copy}, indent=1))
     return 0
 
 
@@ -1273,6 +1314,8 @@ def main() -> int:
     args = parse_args()
     if args.pmc_summary:
         return pmc_summary(*args.pmc_summary)
+    if args.pmc_table:
+        return pmc_table(args.pmc_table)
     if args.prefill_pmc_summary:
         return prefill_pmc_summary(args.prefill_pmc_summary)
     if args.gpus != 1:
