@@ -2,6 +2,8 @@
 // histogram) -> select (top-k + F merge) -> gather-free attend (+ split-K merge), launched in order on the caller's
 // stream with the intermediate scores, select scratch and row list in a caller-provided workspace. Counterpart of
 // sparse_decode_step_kernel (decode.py:145-163).
+#include <algorithm>
+
 #include "common.h"
 #include "select.h"
 
@@ -16,11 +18,19 @@ struct Layout {
     int64_t score_stride;
 };
 
-// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | select scratch (the
-// tiled select's bitmaps and candidate entries, and for k past the LDS sort the score-order sort's buffers, sized for
-// score order so either order fits) | partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state (first-digit histograms and
-// candidate counters, which must start at zero) lives in its own buffer: a region inside this shape-dependent layout
-// would overlap other data of a differently shaped earlier call.
+// Workspace layout: scores [BG, round_up(M, 4)] fp32 | rows [BG, S] int32 | u [BG, 32] fp32 | select scratch: either
+// the tiled select's bitmaps and candidate entries (and for k past the LDS sort the score-order sort's buffers, sized
+// for score order so either order fits) or the score kernel's per-workgroup key lists, whichever is larger, since a
+// step uses one of them | partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state
+// (first-digit histograms, which must start at zero) lives in its own buffer: a region inside this shape-dependent
+// layout would overlap other data of a differently shaped earlier call.
+int64_t list_region_bytes(int64_t BG, int lo, int hi, int k) {
+    if (hi <= lo || k <= 0) return 0;
+    const attnlab::FusedGeometry g = attnlab::fused_tiling((int)BG, lo, hi);
+    const attnlab::ListPlan p = attnlab::list_plan(hi - lo, k, g);
+    return p.cap > 0 ? attnlab::list_bytes((int)BG, g, p) : 0;
+}
+
 Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     Layout L{};
     const int64_t BG = (int64_t)B * G;
@@ -31,7 +41,8 @@ Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     L.rows = align_up(k > 0 ? BG * L.score_stride * 4 : 0);
     L.u = L.rows + align_up(BG * S * 4);
     L.sel = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
-    L.part = L.sel + align_up(k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M, k, ATTNLAB_ORDER_SCORE) : 0);
+    const int64_t sel = k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M, k, ATTNLAB_ORDER_SCORE) : 0;
+    L.part = L.sel + align_up(std::max(sel, list_region_bytes(BG, lo, hi, k)));
     L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
     return L;
 }
@@ -45,13 +56,15 @@ extern "C" int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, 
 
 namespace {
 
-// The launches of one step after the argument checks; score(ws_u, scores, stride, state) runs the score stage for the
-// index table's dtype.
+// The launches of one step after the argument checks; score(ws_u, scores, stride, state, lists) runs the score stage
+// for the index table's dtype. `geo` is the one-launch score's tiling when the score stage runs it (bf16 tables), else
+// nsub == 0; with it, and where list_plan applies, the score kernel also writes per-workgroup key lists and the list
+// select replaces the tiled select.
 template <typename Score>
 int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uint16_t* V, bool has_k_new, int B,
                             int G, int h, int C, int lo, int hi, int legal, int k, float scale, int order, int P,
                             uint32_t* state, void* workspace, int64_t workspace_bytes, int32_t* rows_out,
-                            int64_t* rows_flat, uint16_t* out, void* stream, Score score) {
+                            int64_t* rows_flat, uint16_t* out, void* stream, attnlab::FusedGeometry geo, Score score) {
     using namespace attnlab;
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
@@ -77,19 +90,32 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
     const int S = lo + (legal - hi) + k;
     const int d = 128;
+    // the list select: lists (entries, then headers) in the select scratch region
+    const ListPlan plan = k > 0 ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
+    ScoreLists lists{nullptr, nullptr, plan.lmin, plan.cap};
+    if (plan.cap > 0) {
+        const int64_t eb = list_bytes(B * G, geo, ListPlan{plan.lmin, plan.cap}) - align_up((int64_t)B * G * geo.tiles * 8);
+        lists.entries = reinterpret_cast<uint2*>(ws + L.sel);
+        lists.hdr = reinterpret_cast<uint2*>(ws + L.sel + eb);
+    }
     int rc;
     if (k > 0) {
         // u goes to the workspace (the score kernels that build it in-kernel also store it there)
-        rc = score(reinterpret_cast<float*>(ws + L.u), scores, L.score_stride, lo, hi, state, s);
+        rc = score(reinterpret_cast<float*>(ws + L.u), scores, L.score_stride, lo, hi, state,
+                   plan.cap > 0 ? &lists : nullptr, s);
     } else if (has_k_new) {
         // no candidate is read this step, but the newest key still gets its index column (empty scan range)
-        rc = score(nullptr, nullptr, 0, lo, lo, nullptr, s);
+        rc = score(nullptr, nullptr, 0, lo, lo, nullptr, nullptr, s);
     } else {
         rc = ATTNLAB_OK;
     }
     if (rc) return rc;
-    rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
-                          k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
+    if (plan.cap > 0)
+        rc = select_lists_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
+                               lists, geo, s);
+    else
+        rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
+                              k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
     if (rc) return rc;
     return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
 }
@@ -105,9 +131,11 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     return sparse_decode_step_impl(
         q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
         workspace_bytes, rows_out, rows_flat, out, stream,
-        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, hipStream_t s) {
+        attnlab::fused_geometry(B * G, C, r, h * 128, lo, hi, zT, false),
+        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists* ls,
+            hipStream_t s) {
             return attnlab::score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r, C,
-                                               128, h * 128, slo, shi, write_col, 1, st, s);
+                                               128, h * 128, slo, shi, write_col, 1, st, s, ls);
         });
 }
 
@@ -119,8 +147,9 @@ extern "C" int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const floa
                                               int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
     return sparse_decode_step_impl(
         q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
-        workspace_bytes, rows_out, rows_flat, out, stream,
-        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, hipStream_t s) {
+        workspace_bytes, rows_out, rows_flat, out, stream, attnlab::FusedGeometry{0, 0},
+        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists*,
+            hipStream_t s) {
             return attnlab::score_grouped_f32_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r,
                                                    C, 128, h * 128, slo, shi, write_col, st, s);
         });

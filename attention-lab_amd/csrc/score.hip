@@ -32,6 +32,7 @@ struct ScoreArgs {
     int G, r, C, d, hd, lo, M, write_col;
     int tiles;              // column tiles per (b, g) row
     uint32_t* hist;         // [BG, kSelectStateWords] select state: first-digit histogram bins first, or null
+    ScoreLists lists;       // per-workgroup key lists (entries null: none; score_scan_fused only)
 };
 
 constexpr int kMaxR = 32;
@@ -363,6 +364,8 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     __syncthreads();
 
     float* o = a.out + (size_t)bg * a.out_stride - lo;
+    uint32_t lkey[2 * NSUB];   // this thread's keys (columns cb0 + s * sstride + 2 tid + e), kept for the list
+    uint32_t lvalid = 0u;
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
         if (s + 1 < NSUB) load(s + 1, vb[(s + 1) & 1]);
@@ -392,13 +395,17 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         const float2 p3 = *reinterpret_cast<const float2*>(&part[3][cc]);
         const float s0 = (p0.x + p1.x) + (p2.x + p3.x), s1 = (p0.y + p1.y) + (p2.y + p3.y);
         const int c = cb0 + s * sstride + cc;
+        lkey[2 * s] = score_key(s0);
+        lkey[2 * s + 1] = score_key(s1);
         if (c >= lo && c < hi) {
             o[c] = s0;
-            if (a.hist) atomicAdd(&hsh[score_key(s0) >> kHistShift], 1u);
+            lvalid |= 1u << (2 * s);
+            if (a.hist) atomicAdd(&hsh[lkey[2 * s] >> kHistShift], 1u);
         }
         if (c + 1 >= lo && c + 1 < hi) {
             o[c + 1] = s1;
-            if (a.hist) atomicAdd(&hsh[score_key(s1) >> kHistShift], 1u);
+            lvalid |= 2u << (2 * s);
+            if (a.hist) atomicAdd(&hsh[lkey[2 * s + 1] >> kHistShift], 1u);
         }
         if (s + 1 < NSUB) __syncthreads();   // part is rewritten by the next sub-tile
     }
@@ -412,6 +419,32 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         }
     }
     if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
+    if (a.lists.entries) {
+        // the list: every key of the tile whose first digit is at least that of the tile's lmin-th largest key, placed
+        // by a block scan of the per-thread counts (part is free: the flush's barrier follows its last read)
+        uint32_t* scr = reinterpret_cast<uint32_t*>(&part[0][0]);
+        const uint32_t dl = digit_of_rank(hsh, (uint32_t)a.lists.lmin, scr);
+        uint32_t m = 0u;
+#pragma unroll
+        for (int i = 0; i < 2 * NSUB; ++i) m |= (uint32_t)(((lvalid >> i) & 1u) && (lkey[i] >> kHistShift) >= dl) << i;
+        const uint32_t n = (uint32_t)__popc(m);
+        const uint32_t inc = wave_incl_scan(n);
+        if (lane == 63) scr[1 + wave] = inc;
+        __syncthreads();
+        const uint32_t w0 = scr[1], w1 = scr[2], w2 = scr[3], w3 = scr[4];
+        uint32_t pos = inc - n + (wave > 0 ? w0 : 0u) + (wave > 1 ? w1 : 0u) + (wave > 2 ? w2 : 0u);
+        const int cap = a.lists.cap;
+        uint2* ent = a.lists.entries + ((size_t)bg * a.tiles + tile) * cap;
+#pragma unroll
+        for (int i = 0; i < 2 * NSUB; ++i) {
+            if ((m >> i) & 1u) {
+                const int c = cb0 + (i >> 1) * sstride + 2 * tid + (i & 1);
+                if (pos < (uint32_t)cap) ent[pos] = make_uint2((uint32_t)(c - lo), lkey[i]);
+                ++pos;
+            }
+        }
+        if (tid == 0) a.lists.hdr[(size_t)bg * a.tiles + tile] = make_uint2(dl, (w0 + w1) + (w2 + w3));
+    }
 }
 
 // 2-byte-load scan for tables whose rows are not 16-byte aligned: thread -> 8 adjacent columns from lo, never
@@ -726,10 +759,16 @@ extern "C" int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const 
                               write_col, vector, hist, reinterpret_cast<hipStream_t>(stream));
 }
 
+FusedGeometry attnlab::fused_geometry(int BG, int C, int r, int hd, int lo, int hi, const void* zT, bool u_given) {
+    const bool v16_table = (C % 8 == 0) && (reinterpret_cast<uintptr_t>(zT) % 16 == 0);
+    if (u_given || !v16_table || r != 32 || hd > 512 || hi <= lo) return FusedGeometry{0, 0};
+    return fused_tiling(BG, lo, hi);
+}
+
 int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                                 const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride,
                                 int B, int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector,
-                                uint32_t* hist, hipStream_t s) {
+                                uint32_t* hist, hipStream_t s, const ScoreLists* lists) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
     ATTNLAB_REQUIRE(r >= 1 && r <= kMaxR, "index width r=%d outside [1, %d]", r, kMaxR);
     ATTNLAB_REQUIRE(C >= 1, "C=%d must be positive", C);
@@ -746,7 +785,8 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
     }
     const int M = hi - lo;
     ATTNLAB_REQUIRE(M == 0 || (out != nullptr && out_stride >= M), "out must hold M=%d scores per row", M);
-    ScoreArgs a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 1, hist};
+    ScoreArgs a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 1, hist,
+                ScoreLists{nullptr, nullptr, 0, 0}};
     const bool vec = vector && (C % 4 == 0) && (reinterpret_cast<uintptr_t>(zT) % 8 == 0);
     // the r == 32 prologue reads wq_t with 16-byte loads
     if (r == 32 && u_in == nullptr)
@@ -758,17 +798,19 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
         return check_launch("score_prologue");
     }
     const bool v16_table = vec && (C % 8 == 0) && (reinterpret_cast<uintptr_t>(zT) % 16 == 0);
-    if (u_in == nullptr && v16_table && r == 32 && hd <= 512) {
-        // one launch: u and the z column inside the scan. Sub-tiles per workgroup: as many as keep at least
-        // kFusedMinBlocks workgroups (8 per CU) in the grid.
-        constexpr int kFusedMinBlocks = 2048;
-        const int span = ((hi + 7) & ~7) - (lo & ~7);
-        const int64_t blocks512 = (int64_t)BG * ((span + 511) / 512);
-        const int nsub = blocks512 >= 4 * kFusedMinBlocks ? 4 : blocks512 >= 2 * kFusedMinBlocks ? 2 : 1;
-        a.tiles = (span + 512 * nsub - 1) / (512 * nsub);
+    const FusedGeometry geo = fused_geometry(BG, C, r, hd, lo, hi, zT, u_in != nullptr);
+    if (lists) {
+        ATTNLAB_REQUIRE(vec && geo.nsub > 0 && hist != nullptr && lists->entries && lists->hdr &&
+                            lists->lmin >= 1 && lists->cap >= 1 && lists->cap <= 512 * geo.nsub,
+                        "key lists need the one-launch score (r = 32, h*d <= 512, aligned table) and a select state");
+        a.lists = *lists;
+    }
+    if (vec && geo.nsub > 0) {
+        // one launch: u and the z column inside the scan
+        a.tiles = geo.tiles;
         const dim3 grid(BG * a.tiles), block(256);
-        if (nsub == 4) hipLaunchKernelGGL(score_scan_fused<4>, grid, block, 0, s, a);
-        else if (nsub == 2) hipLaunchKernelGGL(score_scan_fused<2>, grid, block, 0, s, a);
+        if (geo.nsub == 4) hipLaunchKernelGGL(score_scan_fused<4>, grid, block, 0, s, a);
+        else if (geo.nsub == 2) hipLaunchKernelGGL(score_scan_fused<2>, grid, block, 0, s, a);
         else hipLaunchKernelGGL(score_scan_fused<1>, grid, block, 0, s, a);
         return check_launch("score_scan_fused");
     }

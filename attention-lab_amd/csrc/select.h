@@ -2,6 +2,8 @@
 // per-row histogram the score kernel builds for the select kernel in the fused decode step.
 #pragma once
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace attnlab {
@@ -55,6 +57,47 @@ __device__ __forceinline__ void clear_histogram(uint32_t* hsh) {
     for (int b = threadIdx.x; b < kHistBins; b += BLOCK) hsh[b] = 0u;
 }
 
+// First digit of the rank-th largest key of a block's first-digit histogram (0 when it holds fewer keys), found by wave
+// 0 (lane l sums 32 bins from the top, a DPP scan finds the chunk, a second scan its bin) and returned to every thread
+// through `bcast`. Every thread of the block calls it; it ends with one barrier.
+__device__ __forceinline__ uint32_t digit_of_rank(const uint32_t* hist, uint32_t rank, uint32_t* bcast) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int top = kHistBins - 32 * (lane + 1);   // lane 0: the highest 32 bins
+        uint32_t sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hist + top + 4 * ((lane + i) & 7));
+            sum += (v.x + v.y) + (v.z + v.w);
+        }
+        const uint32_t inc = wave_incl_scan(sum);
+        const uint64_t m = __ballot(inc >= rank);
+        uint32_t d = 0u;
+        if (m != 0) {
+            const int l0 = __ffsll((unsigned long long)m) - 1;
+            const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), l0);
+            const int hib = kHistBins - 32 * l0 - 1;   // highest bin of that chunk
+            const uint32_t c = lane < 32 ? hist[hib - lane] : 0u;
+            const uint32_t inc2 = wave_incl_scan(c) + above;
+            const uint64_t m2 = __ballot(lane < 32 && inc2 >= rank);
+            d = (uint32_t)(hib - (__ffsll((unsigned long long)m2) - 1));
+        }
+        if (lane == 0) *bcast = d;
+    }
+    __syncthreads();
+    return *bcast;
+}
+
+// Per-workgroup key lists of the fused decode step (the score kernel writes them, the list select reads them): for
+// each score workgroup of a row, every key of its tile whose first digit is at least the digit of its lmin-th largest
+// key, as (candidate index, key) pairs, and a header (that digit, the list's length; a length above cap means the
+// list was cut and its tile must be read in full).
+struct ScoreLists {
+    uint2* entries;   // [B*G, tiles, cap]
+    uint2* hdr;       // [B*G, tiles]
+    int lmin, cap;
+};
+
 // The argument checks of attnlab_select_rows (the decode step runs them before its first launch, so a rejected call
 // leaves the select state untouched).
 int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
@@ -70,11 +113,59 @@ int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, in
 // score order and k exceeds what the LDS sort holds (no zeroing needed).
 int64_t select_scratch_bytes(int R, int M, int k, int order);
 
-// attnlab_score_grouped with an optional select-state output: per row, the first-digit histogram of the scores.
+// attnlab_score_grouped with an optional select-state output: per row, the first-digit histogram of the scores; and,
+// with `lists` (only where fused_geometry applies and hist is given), the per-workgroup key lists.
 int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                        const uint16_t* wq_t, const float* u_in, float* u_out, float* out, int64_t out_stride, int B,
                        int G, int r, int C, int d, int hd, int lo, int hi, int write_col, int vector, uint32_t* hist,
-                       hipStream_t stream);
+                       hipStream_t stream, const ScoreLists* lists = nullptr);
+
+// The one-launch score's tiling of a row (u, z column and scan in one kernel): sub-tiles of 512 columns per workgroup
+// and workgroups per row; nsub == 0 when that kernel does not apply (u given, unaligned table, r != 32, h*d > 512).
+struct FusedGeometry {
+    int nsub, tiles;
+};
+// Sub-tiles per workgroup: as many as keep at least 2048 workgroups (8 per CU) in the grid.
+inline FusedGeometry fused_tiling(int BG, int lo, int hi) {
+    constexpr int kFusedMinBlocks = 2048;
+    const int span = ((hi + 7) & ~7) - (lo & ~7);
+    const int64_t blocks512 = (int64_t)BG * ((span + 511) / 512);
+    const int nsub = blocks512 >= 4 * kFusedMinBlocks ? 4 : blocks512 >= 2 * kFusedMinBlocks ? 2 : 1;
+    return FusedGeometry{nsub, (span + 512 * nsub - 1) / (512 * nsub)};
+}
+FusedGeometry fused_geometry(int BG, int C, int r, int hd, int lo, int hi, const void* zT, bool u_given);
+
+// The list select's sizing for rows of M candidates and a top-k of k under the score tiling `g`: a workgroup's list
+// holds at least lmin keys (its even share s of the k plus 3 sqrt(s) + 16, so that a list misses part of the row's
+// selection only when its tile holds several standard deviations more than its share), and at most cap (lmin plus
+// 192, for the keys of the first-digit bin holding the lmin-th key). cap == 0: the list select does not apply (rows
+// past 32768 candidates or 128 tiles, or lists that would hold half a tile or more).
+constexpr int kListMaxM = 32768;
+constexpr int kListMaxTiles = 128;
+struct ListPlan {
+    int lmin, cap;
+};
+inline ListPlan list_plan(int M, int k, FusedGeometry g) {
+    if (g.nsub == 0 || k <= 0 || M > kListMaxM || g.tiles > kListMaxTiles) return ListPlan{0, 0};
+    const int nw = 512 * g.nsub;
+    const int64_t share = ((int64_t)k * nw + M - 1) / M;
+    int64_t root = 0;
+    while ((root + 1) * (root + 1) <= share) ++root;
+    const int64_t lmin = share + 3 * root + 16;
+    if (2 * lmin > nw) return ListPlan{0, 0};
+    return ListPlan{(int)lmin, (int)std::min<int64_t>(nw, (lmin + 192 + 63) / 64 * 64)};
+}
+// Bytes of the lists (entries, then headers, 256-byte aligned) for R rows.
+inline int64_t list_bytes(int R, FusedGeometry g, ListPlan p) {
+    const int64_t e = (int64_t)R * g.tiles * p.cap * 8;
+    return (e + 255) / 256 * 256 + ((int64_t)R * g.tiles * 8 + 255) / 256 * 256;
+}
+
+// The list select of the fused decode step: from the score kernel's per-workgroup lists (and the full tile scores of
+// any list that cannot hold the row's selection), the top-k and F as attnlab_select_rows writes them; one launch.
+int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
+                      int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                      const ScoreLists& lists, FusedGeometry geo, hipStream_t stream);
 
 // attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,

@@ -274,3 +274,62 @@ def test_a_fixed_set_other_than_the_rule_is_refused(gpu):
                                   req.off_lo.clone(), lo, hi, k, S)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def _shape_scores(zT, lo, hi, case):
+    """Candidate columns [lo, hi) of the index table rearranged so the score distribution stresses the list select:
+    one tile far above the rest (its list cannot hold its share of the selection and the tile is read in full), every
+    score equal (one first-digit bin holds the row: ties in index order, or the streaming select past 8192 keys), and
+    seven distinct values (ties at the threshold across every list)."""
+    M = hi - lo
+    if case == "skewed_tile":
+        zT[..., lo + M // 5: lo + M // 5 + 700] *= 4            # exact in bf16
+        zT[..., hi - 300: hi] *= 2
+    elif case == "all_equal":
+        zT[..., lo:hi] = zT[..., lo:lo + 1].expand(*zT.shape[:-1], M)
+    elif case == "seven_values":
+        src = lo + (torch.arange(M, device=zT.device) * 5) % 7
+        zT[..., lo:hi] = zT[..., src]
+    else:
+        raise ValueError(case)
+
+
+@pytest.mark.parametrize("case", ["skewed_tile", "all_equal", "seven_values"])
+@pytest.mark.parametrize("B,h,C,L,rho", [
+    (2, 2, 8192 + 64, 8192, 1 / 8),       # one 512-column sub-tile per score workgroup, M < 8192
+    (1, 2, 16384 + 64, 16384, 1 / 16),    # M > 8192: an all-equal row overflows the LDS candidates
+    (16, 4, 16384, 16384, 1 / 32),        # two sub-tiles per score workgroup
+])
+def test_list_select_on_hard_distributions(gpu, case, B, h, C, L, rho):
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L + B)
+    req0 = prepare_request(B, 8, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi = req0.layout.candidate_lo, req0.layout.candidate_hi
+    _shape_scores(zT, lo, hi, case)
+    for canonical in (True, False):
+        z = zT.clone()
+        req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, z, idx, L, rho, canonical)
+        k = req.k
+        s = kernel_scores(z, q_pre, idx, lo, hi)
+        want = exact.select_rows(s, lo, hi, L, k, order="position" if canonical else "score")
+        assert np.array_equal(pos, want), f"{case} canonical={canonical}: row list differs from the oracle"
+        if canonical:
+            ref = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), want)
+            check_out(out, ref, case)
+
+
+def test_list_select_state_is_left_clean(gpu):
+    """After steps through the list select (including a row that falls back to the streaming select), a step with
+    other shapes on the same select state is still bit-exact."""
+    from attention_lab import decode as dec
+    for B, C, L, rho, case in ((1, 16384 + 64, 16384, 1 / 16, "all_equal"), (2, 8192 + 64, 8192, 1 / 8, None),
+                               (1, 2048 + 64, 2048, 1 / 32, None)):
+        K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=2, C=C, seed=C)
+        req0 = prepare_request(B, 8, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+        lo, hi = req0.layout.candidate_lo, req0.layout.candidate_hi
+        if case:
+            _shape_scores(zT, lo, hi, case)
+        req, _, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, False)
+        s = kernel_scores(zT, q_pre, idx, lo, hi)
+        assert np.array_equal(pos, exact.select_rows(s, lo, hi, L, req.k, order="score"))
+        state = dec._STEP_WS.bytes(gpu, 0, "state")
+        assert int(state.abs().sum()) == 0, "the select left its state dirty"
