@@ -15,7 +15,7 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
 SELECT_STATE_WORDS = 2112
@@ -43,6 +43,9 @@ SIGNATURES = {
     "attnlab_topk_tiled": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p, _p, _i64, _p]),
     "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
     "attnlab_select_scratch_bytes": (_i64, [_i] * 4),
+    "attnlab_list_bytes": (_i64, [_i] * 5),
+    "attnlab_score_grouped_lists": (_i, [_p] * 7 + [_i64] + [_i] * 10 + [_p, _p, _i64, _p]),
+    "attnlab_select_lists": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_attend_paged": (_i, [_p, _p, _i, _i, _p, _i64, _i, _p, _p, _i64] + [_i] * 5 + [_f, _p, _i, _p, _p]),

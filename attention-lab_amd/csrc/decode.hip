@@ -24,13 +24,6 @@ struct Layout {
 // step uses one of them | partials [BG, P, h, 130] fp32. Nothing here needs to start at zero. The select state
 // (first-digit histograms, which must start at zero) lives in its own buffer: a region inside this shape-dependent
 // layout would overlap other data of a differently shaped earlier call.
-int64_t list_region_bytes(int64_t BG, int lo, int hi, int k) {
-    if (hi <= lo || k <= 0) return 0;
-    const attnlab::FusedGeometry g = attnlab::fused_tiling((int)BG, lo, hi);
-    const attnlab::ListPlan p = attnlab::list_plan(hi - lo, k, g);
-    return p.cap > 0 ? attnlab::list_bytes((int)BG, g, p) : 0;
-}
-
 Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     Layout L{};
     const int64_t BG = (int64_t)B * G;
@@ -42,7 +35,7 @@ Layout layout_of(int B, int G, int h, int lo, int hi, int legal, int k, int P) {
     L.u = L.rows + align_up(BG * S * 4);
     L.sel = L.u + align_up(k > 0 ? BG * 32 * 4 : 0);
     const int64_t sel = k > 0 ? attnlab::select_scratch_bytes((int)BG, (int)M, k, ATTNLAB_ORDER_SCORE) : 0;
-    L.part = L.sel + align_up(std::max(sel, list_region_bytes(BG, lo, hi, k)));
+    L.part = L.sel + align_up(std::max(sel, attnlab::list_region_bytes(BG, lo, hi, k)));
     L.total = L.part + align_up(P > 1 ? BG * P * h * 130 * 4 : 0);
     return L;
 }
@@ -90,14 +83,9 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
     const int S = lo + (legal - hi) + k;
     const int d = 128;
-    // the list select: lists (entries, then headers) in the select scratch region
-    const ListPlan plan = k > 0 ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
-    ScoreLists lists{nullptr, nullptr, plan.lmin, plan.cap};
-    if (plan.cap > 0) {
-        const int64_t eb = list_bytes(B * G, geo, ListPlan{plan.lmin, plan.cap}) - align_up((int64_t)B * G * geo.tiles * 8);
-        lists.entries = reinterpret_cast<uint2*>(ws + L.sel);
-        lists.hdr = reinterpret_cast<uint2*>(ws + L.sel + eb);
-    }
+    // the list select (it needs the select state): lists in the select scratch region
+    const ListPlan plan = k > 0 && state ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
+    const ScoreLists lists = plan.cap > 0 ? list_layout(ws + L.sel, B * G, geo, plan) : ScoreLists{};
     int rc;
     if (k > 0) {
         // u goes to the workspace (the score kernels that build it in-kernel also store it there)

@@ -224,6 +224,7 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
     __shared__ float u_sh[32];
     __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     __shared__ __attribute__((aligned(16))) float part[4][kCols];
+    __shared__ uint32_t lcount[2];   // the key list: entries placed, waves done
     const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
     const int bg = lin / a.tiles;
     const int tile = lin - bg * a.tiles;
@@ -298,6 +299,7 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     constexpr int kUIter = 512 / 64;   // q_cat features per lane
     __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     __shared__ __attribute__((aligned(16))) float part[4][kCols];
+    __shared__ uint32_t lcount[2];   // the key list: entries placed, waves done
     const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
     const int bg = lin / a.tiles;
     const int tile = lin - bg * a.tiles;
@@ -361,6 +363,7 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         }
     }
     if (a.hist) clear_histogram<256>(hsh);
+    if (tid < 2) lcount[tid] = 0u;
     __syncthreads();
 
     float* o = a.out + (size_t)bg * a.out_stride - lo;
@@ -420,19 +423,19 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     }
     if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
     if (a.lists.entries) {
-        // the list: every key of the tile whose first digit is at least that of the tile's lmin-th largest key, placed
-        // by a block scan of the per-thread counts (part is free: the flush's barrier follows its last read)
-        uint32_t* scr = reinterpret_cast<uint32_t*>(&part[0][0]);
-        const uint32_t dl = digit_of_rank(hsh, (uint32_t)a.lists.lmin, scr);
+        // the list: every key of the tile whose first digit is at least that of the tile's lmin-th largest key (each
+        // wave finds that digit itself; the flush's barrier follows the last histogram update), in no particular
+        // order: a wave reserves its entries with one LDS atomic. The wave that finishes last writes the header.
+        const uint32_t dl = wave_digit_of_rank(hsh, (uint32_t)a.lists.lmin);
         uint32_t m = 0u;
 #pragma unroll
         for (int i = 0; i < 2 * NSUB; ++i) m |= (uint32_t)(((lvalid >> i) & 1u) && (lkey[i] >> kHistShift) >= dl) << i;
         const uint32_t n = (uint32_t)__popc(m);
         const uint32_t inc = wave_incl_scan(n);
-        if (lane == 63) scr[1 + wave] = inc;
-        __syncthreads();
-        const uint32_t w0 = scr[1], w1 = scr[2], w2 = scr[3], w3 = scr[4];
-        uint32_t pos = inc - n + (wave > 0 ? w0 : 0u) + (wave > 1 ? w1 : 0u) + (wave > 2 ? w2 : 0u);
+        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+        uint32_t base = 0u;
+        if (lane == 0) base = atomicAdd(&lcount[0], tot);
+        uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)base, 0) + inc - n;
         const int cap = a.lists.cap;
         uint2* ent = a.lists.entries + ((size_t)bg * a.tiles + tile) * cap;
 #pragma unroll
@@ -443,7 +446,12 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
                 ++pos;
             }
         }
-        if (tid == 0) a.lists.hdr[(size_t)bg * a.tiles + tile] = make_uint2(dl, (w0 + w1) + (w2 + w3));
+        // acquire-release at workgroup scope: this wave's reservation is ordered before its "done", and the count read
+        // after the fourth wave's "done"
+        if (lane == 0 &&
+            __hip_atomic_fetch_add(&lcount[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP) == 256 / 64 - 1)
+            a.lists.hdr[(size_t)bg * a.tiles + tile] =
+                make_uint2(dl, __hip_atomic_load(&lcount[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     }
 }
 
@@ -837,6 +845,33 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
         hipLaunchKernelGGL(score_scan_scalar<256>, dim3(BG * a.tiles), dim3(256), 0, s, a);
     }
     return check_launch("score_scan");
+}
+
+extern "C" int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k) {
+    if (B < 1 || G < 1 || lo < 0 || hi < lo || k < 0 || k > hi - lo) return -1;
+    return list_region_bytes((int64_t)B * G, lo, hi, k);
+}
+
+extern "C" int attnlab_score_grouped_lists(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk,
+                                           const uint16_t* q_cat, const uint16_t* wq_t, float* u_out, float* out,
+                                           int64_t out_stride, int B, int G, int r, int C, int d, int hd, int lo,
+                                           int hi, int write_col, int k, uint32_t* state, void* lists,
+                                           int64_t lists_bytes, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && 0 <= lo && lo <= hi && 0 <= k && k <= hi - lo,
+                    "need B, G >= 1, 0 <= lo <= hi and 0 <= k <= hi - lo (B=%d G=%d lo=%d hi=%d k=%d)", B, G, lo, hi, k);
+    const FusedGeometry geo = fused_geometry(B * G, C, r, hd, lo, hi, zT, false);
+    const ListPlan plan = list_plan(hi - lo, k, geo);
+    ATTNLAB_REQUIRE(plan.cap > 0, "the list select does not apply: it needs the one-launch score (r = 32, h*d <= 512, "
+                    "a 16-byte aligned table with C %% 8 == 0), hi - lo <= %d and k small against hi - lo", kListMaxM);
+    ATTNLAB_REQUIRE(state != nullptr && (reinterpret_cast<uintptr_t>(state) & 15) == 0,
+                    "the key lists need a 16-byte aligned select state");
+    ATTNLAB_REQUIRE(lists != nullptr && (reinterpret_cast<uintptr_t>(lists) & 255) == 0 &&
+                        lists_bytes >= list_bytes(B * G, geo, plan),
+                    "lists must be 256-byte aligned and hold attnlab_list_bytes = %lld bytes",
+                    (long long)list_bytes(B * G, geo, plan));
+    const ScoreLists ls = list_layout(lists, B * G, geo, plan);
+    return score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_out, out, out_stride, B, G, r, C, d, hd, lo, hi,
+                              write_col, 1, state, reinterpret_cast<hipStream_t>(stream), &ls);
 }
 
 extern "C" int attnlab_score_prologue(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,

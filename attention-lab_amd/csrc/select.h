@@ -57,35 +57,29 @@ __device__ __forceinline__ void clear_histogram(uint32_t* hsh) {
     for (int b = threadIdx.x; b < kHistBins; b += BLOCK) hsh[b] = 0u;
 }
 
-// First digit of the rank-th largest key of a block's first-digit histogram (0 when it holds fewer keys), found by wave
-// 0 (lane l sums 32 bins from the top, a DPP scan finds the chunk, a second scan its bin) and returned to every thread
-// through `bcast`. Every thread of the block calls it; it ends with one barrier.
-__device__ __forceinline__ uint32_t digit_of_rank(const uint32_t* hist, uint32_t rank, uint32_t* bcast) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const int top = kHistBins - 32 * (lane + 1);   // lane 0: the highest 32 bins
-        uint32_t sum = 0;
+// First digit of the rank-th largest key of a block's first-digit histogram in LDS (0 when it holds fewer keys),
+// found by one wave on its own: lane l sums the l-th 32 bins from the top (starting at a lane-dependent 16-byte segment,
+// so the lanes spread over the LDS banks), a DPP scan finds the chunk, a second scan its bin. No barrier; every lane of
+// the calling wave gets the digit.
+__device__ __forceinline__ uint32_t wave_digit_of_rank(const uint32_t* hist, uint32_t rank) {
+    const int lane = threadIdx.x & 63;
+    const int top = kHistBins - 32 * (lane + 1);   // lane 0: the highest 32 bins
+    uint32_t sum = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint4 v = *reinterpret_cast<const uint4*>(hist + top + 4 * ((lane + i) & 7));
-            sum += (v.x + v.y) + (v.z + v.w);
-        }
-        const uint32_t inc = wave_incl_scan(sum);
-        const uint64_t m = __ballot(inc >= rank);
-        uint32_t d = 0u;
-        if (m != 0) {
-            const int l0 = __ffsll((unsigned long long)m) - 1;
-            const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), l0);
-            const int hib = kHistBins - 32 * l0 - 1;   // highest bin of that chunk
-            const uint32_t c = lane < 32 ? hist[hib - lane] : 0u;
-            const uint32_t inc2 = wave_incl_scan(c) + above;
-            const uint64_t m2 = __ballot(lane < 32 && inc2 >= rank);
-            d = (uint32_t)(hib - (__ffsll((unsigned long long)m2) - 1));
-        }
-        if (lane == 0) *bcast = d;
+    for (int i = 0; i < 8; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(hist + top + 4 * ((lane + i) & 7));
+        sum += (v.x + v.y) + (v.z + v.w);
     }
-    __syncthreads();
-    return *bcast;
+    const uint32_t inc = wave_incl_scan(sum);
+    const uint64_t m = __ballot(inc >= rank);
+    if (m == 0) return 0u;
+    const int l0 = __ffsll((unsigned long long)m) - 1;
+    const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sum), l0);
+    const int hib = kHistBins - 32 * l0 - 1;   // highest bin of that chunk
+    const uint32_t c = lane < 32 ? hist[hib - lane] : 0u;
+    const uint32_t inc2 = wave_incl_scan(c) + above;
+    const uint64_t m2 = __ballot(lane < 32 && inc2 >= rank);
+    return (uint32_t)(hib - (__ffsll((unsigned long long)m2) - 1));
 }
 
 // Per-workgroup key lists of the fused decode step (the score kernel writes them, the list select reads them): for
@@ -156,9 +150,24 @@ inline ListPlan list_plan(int M, int k, FusedGeometry g) {
     return ListPlan{(int)lmin, (int)std::min<int64_t>(nw, (lmin + 192 + 63) / 64 * 64)};
 }
 // Bytes of the lists (entries, then headers, 256-byte aligned) for R rows.
+inline int64_t list_entry_bytes(int R, FusedGeometry g, ListPlan p) {
+    return ((int64_t)R * g.tiles * p.cap * 8 + 255) / 256 * 256;
+}
 inline int64_t list_bytes(int R, FusedGeometry g, ListPlan p) {
-    const int64_t e = (int64_t)R * g.tiles * p.cap * 8;
-    return (e + 255) / 256 * 256 + ((int64_t)R * g.tiles * 8 + 255) / 256 * 256;
+    return list_entry_bytes(R, g, p) + ((int64_t)R * g.tiles * 8 + 255) / 256 * 256;
+}
+// The list region of R rows of candidates [lo, hi) with a top-k of k (0: the list select does not apply), and the
+// lists laid out in a region at `base`.
+inline int64_t list_region_bytes(int64_t R, int lo, int hi, int k) {
+    if (hi <= lo || k <= 0) return 0;
+    const FusedGeometry g = fused_tiling((int)R, lo, hi);
+    const ListPlan p = list_plan(hi - lo, k, g);
+    return p.cap > 0 ? list_bytes((int)R, g, p) : 0;
+}
+inline ScoreLists list_layout(void* base, int R, FusedGeometry g, ListPlan p) {
+    char* b = static_cast<char*>(base);
+    return ScoreLists{reinterpret_cast<uint2*>(b), reinterpret_cast<uint2*>(b + list_entry_bytes(R, g, p)), p.lmin,
+                      p.cap};
 }
 
 // The list select of the fused decode step: from the score kernel's per-workgroup lists (and the full tile scores of

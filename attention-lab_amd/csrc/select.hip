@@ -1714,6 +1714,25 @@ extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, in
                             scratch, scratch_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int attnlab_select_lists(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal,
+                                    int k, int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat,
+                                    uint32_t* state, const void* lists, int64_t lists_bytes, void* stream) {
+    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride);
+    if (rc) return rc;
+    const FusedGeometry geo = fused_tiling(B * G, lo, hi);
+    const ListPlan plan = hi > lo ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
+    ATTNLAB_REQUIRE(plan.cap > 0, "the list select does not apply to B*G=%d, M=%d, k=%d", B * G, hi - lo, k);
+    ATTNLAB_REQUIRE(state != nullptr && (reinterpret_cast<uintptr_t>(state) & 15) == 0,
+                    "the list select needs the 16-byte aligned select state");
+    ATTNLAB_REQUIRE(lists != nullptr && (reinterpret_cast<uintptr_t>(lists) & 255) == 0 &&
+                        lists_bytes >= list_bytes(B * G, geo, plan),
+                    "lists must be 256-byte aligned and hold attnlab_list_bytes = %lld bytes",
+                    (long long)list_bytes(B * G, geo, plan));
+    return select_lists_impl(scores, score_stride, B, G, lo, hi, legal, k, C, order, rows, rows_stride, rows_flat,
+                             state, list_layout(const_cast<void*>(lists), B * G, geo, plan), geo,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int64_t attnlab_select_scratch_bytes(int R, int M, int k, int order) {
     if (R < 0 || M < 0 || k < 0 || k > M) return -1;
     return select_scratch_bytes(R, M, k, order);

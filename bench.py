@@ -301,6 +301,9 @@ def launchers(ls, torch):
     hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
     sel_bytes = lib.attnlab_select_scratch_bytes(B * G, ls.M, ls.k, nat.ORDER_POSITION)
     sel_scratch = torch.empty(sel_bytes, dtype=torch.uint8, device=dev)
+    # the list select (what the fused step runs where it applies): the score kernel's key lists
+    list_bytes = lib.attnlab_list_bytes(B, G, ls.lo, ls.hi, ls.k)
+    lists = torch.empty(max(list_bytes, 256), dtype=torch.uint8, device=dev)
     u_buf = torch.zeros(B * G * r, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(d)
 
@@ -318,12 +321,23 @@ def launchers(ls, torch):
         nat.call("attnlab_dense_decode", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(), B, G,
                  h, ls.L, C, Pd, scale, ls.dense_out[l].data_ptr(), 1, part.data_ptr(), stream())
 
-    def score(l):   # u, z column and scan in one launch, as in the fused step: the dominant kernel
+    def score(l):   # u, z column, scan (and the key lists) in one launch, as in the fused step: the dominant kernel
+        if list_bytes > 0:
+            nat.call("attnlab_score_grouped_lists", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
+                     ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), u_buf.data_ptr(), ls.scores.data_ptr(),
+                     ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, ls.k, hist.data_ptr(),
+                     lists.data_ptr(), list_bytes, stream())
+            return
         nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
                  ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), None, u_buf.data_ptr(), ls.scores.data_ptr(),
                  ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1, hist.data_ptr(), stream())
 
     def select(l):
+        if list_bytes > 0:
+            nat.call("attnlab_select_lists", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k,
+                     C, nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), lists.data_ptr(),
+                     list_bytes, stream())
+            return
         nat.call("attnlab_select_rows", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
                  nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), sel_scratch.data_ptr(),
                  sel_bytes, stream())
@@ -339,15 +353,17 @@ def launchers(ls, torch):
 
     return {"sparse": sparse, "dense": dense, "score": score, "select": select, "attend": attend,
             "score_select": score_select, "hist": hist, "partitions": P, "dense_partitions": Pd,
-            "_keep": (ws, part, step_hist, u_buf, sel_scratch)}
+            "select_kernels": "select_lists" if list_bytes > 0 else "select_classify_compact + select_resolve_compact",
+            "_keep": (ws, part, step_hist, u_buf, sel_scratch, lists)}
 
 
 def kernel_breakdown(torch, fns, ls, reps):
     """Per-layer us of each stage of the fused step, from graphs of one launch per layer on consistent data, each
-    stage in forward and reverse layer order (median, p95, conservative): score (u, z column and scan, one kernel),
-    select = (score + select) - score (the select consumes and clears the histogram the scan builds; score-only graphs
-    leave it dirty, so it is zeroed before the pair), attend (+ split-K merge). The flat figures are the conservative
-    medians; `mean` holds the forward-order means (the kernel-trace averages compare with these)."""
+    stage in forward and reverse layer order (median, p95, conservative): score (u, z column, scan and, where the list
+    select applies, its key lists: one kernel), select = (score + select) - score (the select consumes and clears the
+    histogram the scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend (+ split-K
+    merge). The flat figures are the conservative medians; `mean` holds the forward-order means (the kernel-trace
+    averages compare with these)."""
     n = ls.n
     score = ordered_stats(torch, fns["score"], n, reps, 3, per=n)
     fns["hist"].zero_()
@@ -1425,6 +1441,7 @@ def main() -> int:
         "timing": timing,
         "per_layer_us": {"sparse": us_layer, "sparse_conservative": us_layer_cons, "dense": ms_dense * 1e3 / ls.n,
                          "score": kus["score"], "select": kus["select"], "attend_with_combine": kus["attend"],
+                         "select_kernels": fns["select_kernels"],
                          "note": "sparse: the timed region's mean; the kernel figures and dense: conservative medians "
                                  "(slower of forward / reverse layer order); kernel_orders holds every order's median, "
                                  "p95 and mean"},

@@ -193,6 +193,26 @@ int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G,
                         int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
                         void* scratch, int64_t scratch_bytes, void* stream);
 
+/*
+ * The list select, the two stages attnlab_sparse_decode_step runs where it applies (no reference counterpart: the
+ * reference's step is indexer + torch.topk, decode.py:86-93 and :145-163). attnlab_score_grouped_lists is the
+ * one-launch attnlab_score_grouped (bf16 table, r = 32, h*d <= 512, C % 8 == 0, 16-byte aligned zT, u built from q_cat
+ * and wq_t) that also writes, for every score workgroup, a list of its largest keys into `lists` (256-byte aligned,
+ * attnlab_list_bytes(B, G, lo, hi, k) bytes, no initialisation); `state` is required. attnlab_select_lists then
+ * writes what attnlab_select_rows writes for the same scores, state and arguments, reading the lists instead of every
+ * score (a tile whose list cannot hold its part of the selection is read from the scores), in one launch, and leaves
+ * the state zeroed. attnlab_list_bytes returns 0 where the list select does not apply (hi - lo > 32768, or k large
+ * against hi - lo; both functions then fail with ATTNLAB_EINVAL) and -1 for invalid sizes.
+ */
+int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k);
+int attnlab_score_grouped_lists(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
+                                const uint16_t* wq_t, float* u_out, float* out, int64_t out_stride, int B, int G,
+                                int r, int C, int d, int hd, int lo, int hi, int write_col, int k, uint32_t* state,
+                                void* lists, int64_t lists_bytes, void* stream);
+int attnlab_select_lists(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
+                         int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
+                         const void* lists, int64_t lists_bytes, void* stream);
+
 /* Scratch bytes of attnlab_select_rows / attnlab_topk_tiled for R rows of M candidates and top-k in `order`: the
  * tiled select's bitmaps and candidate entries, plus the radix pass's buffers in score order with
  * k > ATTNLAB_LDS_SORT_K (-1 for negative sizes or k outside [0, M]). */

@@ -121,4 +121,24 @@ def test_workspace_size_formula(native_lib):
         assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)
     # the lists outgrow the tiled select's scratch at B = 16, 32K, k = 2048
     assert list_region(128, 4, 32704, 2048) > select_scratch(128, 32700, 2048, 1)
+
+
+def test_list_bytes_formula(native_lib):
+    for B, G, lo, hi, k in ((16, 8, 4, 32704, 1024), (1, 8, 4, 32704, 1024), (1, 8, 4, 1984, 64), (2, 8, 4, 300, 32),
+                            (1, 8, 4, 32704, 16384), (1, 8, 0, 40000, 100), (4, 8, 60, 60, 0), (16, 8, 4, 16320, 512)):
+        assert native_lib.attnlab_list_bytes(B, G, lo, hi, k) == list_region(B * G, lo, hi, k)
+    assert native_lib.attnlab_list_bytes(0, 8, 0, 10, 1) == -1
+    assert native_lib.attnlab_list_bytes(1, 8, 0, 10, 11) == -1
+
+
+def test_list_select_refuses_shapes_it_does_not_cover(native_lib):
+    with pytest.raises(ValueError, match="does not apply"):   # r = 16: not the one-launch score
+        _native.call("attnlab_score_grouped_lists", *([16] * 7), 4096, 1, 8, 16, 4096, 128, 256, 4, 4000, 4095, 100,
+                     16, 256, 1 << 20, None)
+    with pytest.raises(ValueError, match="does not apply"):   # M = 40000 > 32768
+        _native.call("attnlab_select_lists", 16, 40000, 1, 8, 4, 40004, 40068, 100, 40100, 0, 16, 200, None, 16, 256,
+                     1 << 20, None)
+    with pytest.raises(ValueError, match="attnlab_list_bytes"):   # lists too small
+        _native.call("attnlab_select_lists", 16, 2000, 1, 8, 4, 2004, 2068, 64, 2100, 0, 16, 200, None, 16, 256, 64,
+                     None)
     assert native_lib.attnlab_sparse_decode_workspace(0, 8, 2, 4, 100, 164, 3, 1) == -1

@@ -333,3 +333,70 @@ def test_list_select_state_is_left_clean(gpu):
         assert np.array_equal(pos, exact.select_rows(s, lo, hi, L, req.k, order="score"))
         state = dec._STEP_WS.bytes(gpu, 0, "state")
         assert int(state.abs().sum()) == 0, "the select left its state dirty"
+
+
+@pytest.mark.parametrize("B,h,C,L,rho", [(1, 2, 2048 + 64, 2048, 1 / 32), (2, 4, 8192 + 64, 8192, 1 / 8),
+                                         (16, 4, 32768, 32768, 1 / 32)])
+def test_list_select_stages_through_the_abi(gpu, B, h, C, L, rho):
+    """attnlab_score_grouped_lists + attnlab_select_lists, the two stages the step runs: scores equal the step's own
+    score stage, rows are bit-exact against the oracle in both orders and equal the step's, and the state is left zero."""
+    from attention_lab import _native as nat
+    G = 8
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L + 7)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    M = hi - lo
+    nbytes = nat.lib().attnlab_list_bytes(B, G, lo, hi, k)
+    assert nbytes > 0
+    lists = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    qc = q_pre.reshape(B, G, h * 128).contiguous()
+    kn = k_pre_new.reshape(B, G, 128).contiguous()
+    stream = nat.stream_of(gpu)
+    for canonical in (True, False):
+        order = nat.ORDER_POSITION if canonical else nat.ORDER_SCORE
+        z = zT.clone()
+        scores = torch.empty(B * G, M, dtype=torch.float32, device=gpu)
+        rows = torch.empty(B * G, S, dtype=torch.int32, device=gpu)
+        nat.call("attnlab_score_grouped_lists", z.data_ptr(), kn.data_ptr(), idx.wk.data_ptr(), qc.data_ptr(),
+                 idx.wq_t_scaled.data_ptr(), None, scores.data_ptr(), M, B, G, 32, C, 128, h * 128, lo, hi, L - 1, k,
+                 state.data_ptr(), lists.data_ptr(), nbytes, stream)
+        nat.call("attnlab_select_lists", scores.data_ptr(), M, B, G, lo, hi, L, k, C, order, rows.data_ptr(), S, None,
+                 state.data_ptr(), lists.data_ptr(), nbytes, stream)
+        torch.cuda.synchronize()
+        assert int(state.abs().sum()) == 0, "the list select left its state dirty"
+        s = scores.view(B, G, M).cpu().numpy()
+        assert np.array_equal(s, kernel_scores(z, q_pre, idx, lo, hi)), "score stage differs from the step's"
+        want = exact.select_rows(s, lo, hi, L, k, order="position" if canonical else "score")
+        assert np.array_equal(rows.view(B, G, S).cpu().numpy(), want)
+        _, _, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT.clone(), idx, L, rho, canonical)
+        assert np.array_equal(pos, want)
+
+
+def test_step_without_select_state(gpu):
+    """attnlab_sparse_decode_step with a null select state (the select then builds its own histograms) gives the rows
+    and output of a step with one."""
+    from attention_lab import _native as nat
+    B, G, h, C, L = 2, 8, 2, 4096 + 64, 4096
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=5)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=1 / 16, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    ws_bytes = nat.lib().attnlab_sparse_decode_workspace(B, G, h, lo, hi, L, k, 1)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+    state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    qm = q.reshape(B, G, h, 128).contiguous()
+    qc = q_pre.reshape(B, G, h * 128).contiguous()
+    kn = k_pre_new.reshape(B, G, 128).contiguous()
+    res = []
+    for st in (state, None):
+        z = zT.clone()
+        out = torch.empty(B, G, h, 128, dtype=torch.bfloat16, device=gpu)
+        rows = torch.empty(B * G, S, dtype=torch.int32, device=gpu)
+        nat.call("attnlab_sparse_decode_step", qm.data_ptr(), qc.data_ptr(), K.data_ptr(), V.data_ptr(), z.data_ptr(),
+                 idx.wq_t_scaled.data_ptr(), idx.wk.data_ptr(), kn.data_ptr(), B, G, h, 32, C, lo, hi, L, k, L - 1,
+                 1 / np.sqrt(128), nat.ORDER_POSITION, 1, None if st is None else st.data_ptr(), ws.data_ptr(),
+                 ws_bytes, rows.data_ptr(), None, out.data_ptr(), nat.stream_of(gpu))
+        torch.cuda.synchronize()
+        res.append((rows.cpu(), out.cpu()))
+    assert int(state.abs().sum()) == 0
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
