@@ -17,6 +17,7 @@
 // coalesced; longer rows (L = 64K..128K) re-read the row (L2-resident) in every pass.
 #include "common.h"
 #include "select.h"
+#include "select_core.h"
 
 namespace attnlab {
 
@@ -1142,269 +1143,45 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve_compact(SelectArgs
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// List select (the fused decode step, rows of at most kListMaxM candidates): the score kernel leaves, per workgroup of
-// a row, a list of its largest keys (every key whose first digit is at least that of the workgroup's lmin-th largest,
-// d_L) with a header (d_L, length). One 1024-thread workgroup per row then
-//   1. in one round trip loads the row's first-digit histogram, the headers and the first entries of every list (wave
-//      w owns lists w, w + 16, ...); every wave finds b1, the first digit of the k-th largest key, on its own (super-bins
-//      in registers, then the chosen super-bin's 32 bins from LDS);
-//   2. takes, from each list whose d_L <= b1 and whose length fits its capacity (such a list holds every key of its
-//      tile with first digit >= b1), the keys above b1 into the selection bitmap and the keys in bin b1 into a candidate
-//      array (one LDS atomic per wave and pass) while counting their second digit. A list that fails either test is
-//      replaced by its tile's scores (the columns of the score workgroup: sub-tile s covers (lo & ~7) + (s * tiles + w)
-//      * 512 + [0, 512));
-//   3. finds the second digit; when its bin holds exactly the keys still to take (the usual case) the selection is
-//      complete, else a third digit and the first krem tied keys in index order (a tie bitmap and one block scan);
-//      then emits the bitmap as select_resolve_compact does.
-// A bin b1 holding more than kListCandCap keys sends the row to the single-workgroup streaming select. No pass reads
-// the row's scores unless a list was incomplete.
+// List select (the fused decode step, rows of at most kListMaxM candidates): one 1024-thread workgroup per row builds
+// the row's selection bitmap from the score kernel's per-workgroup key lists (list_select_bitmap), then emits it as
+// select_resolve_compact does (F, position or score order) and clears the row's select state.
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int kListCandCap = kMaxScoreOrderK;                      // candidates staged in sortbuf as uint2
-constexpr int kListCandPerThread = kListCandCap / kSelThreads;     // 8
-constexpr int kListSlots = 8;                                      // entries per lane loaded in the first round trip
-static_assert(kListCandCap * sizeof(uint2) <= sizeof(SelectShared::sortbuf), "candidates live in sortbuf");
-static_assert(kListMaxM / 32 == kSelThreads, "one selection bitmap word per thread");
-static_assert(kListMaxTiles <= kSelWaves * kListSlots, "every list gets at least one slot per lane");
+constexpr int kListSlots = 8;   // entries per lane loaded in the first round trip
+static_assert(kListWords == kSelThreads, "one selection bitmap word per thread");
 
 struct ListArgs {
     const uint2* entries;   // [R, tiles, cap]
     const uint2* hdr;       // [R, tiles]
-    int cap, tiles, nsub;
-    int lspl;               // log2 of the first-round-trip slots per lane of each list
+    int cap, tiles, nsub, lspl;
 };
-
-// Slots per lane for each list in the first round trip: the largest power of two with every list of a wave covered
-// (kListSlots / lists per wave); slots past cap are not loaded.
-inline int list_lspl(int tiles) {
-    const int nlw = (tiles + kSelWaves - 1) / kSelWaves;
-    int l = 0;
-    while ((2 << l) <= kListSlots / nlw) ++l;
-    return l;
-}
-
-// b1 and the keys above bin b1 for this wave, from the super-bin counts in registers (lane l: super-bin 63 - l) and
-// the bins in LDS; no barrier. b1 = 0 and above = 0 when the histogram holds fewer than k keys.
-__device__ __forceinline__ uint32_t wave_first_digit(uint32_t sbv, const uint32_t* bins, uint32_t k, uint32_t& above,
-                                                     uint32_t& count) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t inc = wave_incl_scan(sbv);
-    const uint64_t m = __ballot(inc >= k);
-    above = 0u;
-    count = 0u;
-    if (m == 0) return 0u;
-    const int l0 = __ffsll((unsigned long long)m) - 1;
-    const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sbv), l0);
-    const int top = kHistBins - 32 * l0 - 1;   // highest bin of that super-bin
-    const uint32_t c = lane < 32 ? bins[top - lane] : 0u;
-    const uint32_t inc2 = wave_incl_scan(c) + a0;
-    const uint64_t m2 = __ballot(lane < 32 && inc2 >= k);
-    if (m2 == 0) return 0u;
-    const int l1 = __ffsll((unsigned long long)m2) - 1;
-    count = (uint32_t)__builtin_amdgcn_readlane((int)c, l1);
-    above = (uint32_t)__builtin_amdgcn_readlane((int)inc2, l1) - count;
-    return (uint32_t)(top - l1);
-}
 
 __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListArgs t) {
     __shared__ SelectShared sh;   // hist: the first digit's bins; sortbuf: candidates, then score order's pairs
-    // second and third digits' histograms, the selection and tie bitmaps (or the streaming fallback's arrays)
-    __shared__ __attribute__((aligned(16))) uint32_t lds[2048 + 1024 + 2 * kRegWords];
+    __shared__ __attribute__((aligned(16))) uint32_t lds[2048 + 1024 + 2 * kListWords];
     __shared__ uint2 hdr[kListMaxTiles];
-    __shared__ uint32_t sup2[64];   // super-bins of hist2 (32 bins each)
-    __shared__ uint32_t ncand;
-    uint32_t* hist2 = lds;
-    uint32_t* hist3 = lds + 2048;
-    uint32_t* bits = lds + 3072;
-    uint32_t* ties = lds + 3072 + kRegWords;
-    uint2* cand = reinterpret_cast<uint2*>(sh.sortbuf);
+    __shared__ uint32_t sup2[64];
+    __shared__ uint32_t misc[4];
+    static_assert(kListCandCap * sizeof(uint2) <= sizeof(SelectShared::sortbuf), "candidates live in sortbuf");
     const int row = xcd_contiguous_block();   // the XCD whose score workgroups wrote the row
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nt = t.tiles;
-    const int spl = 1 << t.lspl;
-    const uint32_t* st = a.hist + (size_t)row * kSelectStateWords;
-    const uint2* erow = t.entries + (size_t)row * nt * t.cap;
-    // round trip 1: bins (two per thread), this wave's super-bins, the headers, the lists' first entries
-    const uint32_t h0 = st[tid], h1 = st[tid + kSelThreads];
-    const uint32_t sbv = st[kHistBins + (kSuperBins - 1 - lane)];
-    const uint2 hv = tid < nt ? t.hdr[(size_t)row * nt + tid] : make_uint2(0u, 0u);
-    uint2 e[kListSlots];
-#pragma unroll
-    for (int u = 0; u < kListSlots; ++u) {
-        const int w = wave + kSelWaves * (u >> t.lspl), j = 64 * (u & (spl - 1)) + lane;
-        e[u] = w < nt && j < t.cap ? erow[(size_t)w * t.cap + j] : make_uint2(0u, 0u);
-    }
-    sh.hist[tid] = h0;
-    sh.hist[tid + kSelThreads] = h1;
-    if (tid < nt) hdr[tid] = hv;
-    hist2[tid] = 0u;
-    hist2[tid + kSelThreads] = 0u;
-    hist3[tid] = 0u;
-    bits[tid] = 0u;
-    ties[tid] = 0u;
-    if (tid < 64) sup2[tid] = 0u;
-    if (tid == 0) {   // defaults keep every later index in range even for a state that does not match the scores
-        ncand = 0u;
-        sh.digit = 0u;
-        sh.krem = 0u;
-        sh.dcount = 0u;
-    }
-    __syncthreads();
-    uint32_t above, nb1;
-    const uint32_t b1 = wave_first_digit(sbv, sh.hist, (uint32_t)a.k, above, nb1);
-    uint32_t krem = (uint32_t)a.k - above;
-    if (nb1 > (uint32_t)kListCandCap) {   // bin b1 too full for the candidate array (the same test in every wave)
-        __syncthreads();
-        select_row_streaming(a, row, sh, StreamLds{lds, lds + 2048, lds + 3072, lds + 3072 + kRegWords});
-        return;
-    }
-    const uint32_t M = (uint32_t)a.M;
-    // keys of one pass (n per lane, ok bits): above b1 into the bitmap, bin b1 counted (second digit) and appended
-    auto take = [&](const uint32_t* idx, const uint32_t* key, uint32_t ok, int n) {
-        uint32_t cm = 0u;
-        for (int i = 0; i < n; ++i) {
-            const uint32_t ix = min(idx[i], M - 1u);   // in range for any list contents
-            const uint32_t dg = key[i] >> kHistShift;
-            const bool v = (ok >> i) & 1u;
-            if (v && dg > b1) atomicOr(&bits[ix >> 5], 1u << (ix & 31u));
-            if (v && dg == b1) {
-                cm |= 1u << i;
-                const uint32_t d2 = (key[i] >> 10) & 2047u;
-                atomicAdd(&hist2[d2], 1u);
-                atomicAdd(&sup2[d2 >> 5], 1u);
-            }
-        }
-        const uint32_t nc = (uint32_t)__popc(cm);
-        const uint32_t inc = wave_incl_scan(nc);
-        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
-        if (tot == 0) return;
-        uint32_t base = 0u;
-        if (lane == 63) base = atomicAdd(&ncand, tot);
-        uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)base, 63) + inc - nc;
-        for (int i = 0; i < n; ++i) {
-            if ((cm >> i) & 1u) {
-                if (off < (uint32_t)kListCandCap)
-                    cand[off] = make_uint2(min(idx[i], M - 1u), key[i] & ((1u << kHistShift) - 1u));
-                ++off;
-            }
-        }
-    };
-    // step 2: the slots of the first round trip, then what they did not cover (rare)
-    {
-        uint32_t idx[kListSlots], key[kListSlots], ok = 0u;
-#pragma unroll
-        for (int u = 0; u < kListSlots; ++u) {
-            const int w = wave + kSelWaves * (u >> t.lspl), jj = u & (spl - 1);
-            const uint2 h = w < nt ? hdr[w] : make_uint2(0xffffffffu, 0u);
-            const bool complete = h.x <= b1 && h.y <= (uint32_t)t.cap;
-            idx[u] = e[u].x;
-            key[u] = e[u].y;
-            ok |= (uint32_t)(complete && (uint32_t)(64 * jj + lane) < h.y) << u;
-        }
-        take(idx, key, ok, kListSlots);
-    }
-    const float* srow = a.scores + (size_t)row * a.score_stride;
-    for (int w = wave; w < nt; w += kSelWaves) {
-        const uint2 h = hdr[w];
-        if (h.x <= b1 && h.y <= (uint32_t)t.cap) {
-            const uint2* ep = erow + (size_t)w * t.cap;
-            for (int j0 = 64 * spl; j0 < (int)h.y; j0 += 512) {   // entries past the first round trip (h.y <= cap)
-                uint32_t idx[8], key[8], ok = 0u;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int j = j0 + 64 * u + lane;
-                    const uint2 v = j < (int)h.y ? ep[j] : make_uint2(0u, 0u);
-                    idx[u] = v.x;
-                    key[u] = v.y;
-                    ok |= (uint32_t)(j < (int)h.y) << u;
-                }
-                take(idx, key, ok, 8);
-            }
-        } else {
-            // an incomplete list: the tile's scores, lane -> 8 consecutive columns of each sub-tile, every load issued
-            // before the first is used
-            const int cb = (a.lo & ~7) + w * 512 + lane * 8;
-            float v[4][8];
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int c = cb + s * nt * 512 + i;
-                    v[s][i] = s < t.nsub && c >= a.lo && c < a.hi ? srow[c - a.lo] : 0.0f;
-                }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (s >= t.nsub) break;
-                uint32_t idx[8], key[8], ok = 0u;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int c = cb + s * nt * 512 + i;
-                    key[i] = score_key(v[s][i]);
-                    idx[i] = (uint32_t)(c - a.lo);
-                    ok |= (uint32_t)(c >= a.lo && c < a.hi) << i;
-                }
-                take(idx, key, ok, 8);
-            }
-        }
-    }
-    __syncthreads();
-    // step 3: the second digit over every key of bin b1, found by every wave on its own as b1 was
-    uint32_t above2, n2;
-    const uint32_t d2 = wave_first_digit(sup2[63 - lane], hist2, krem, above2, n2);
-    krem -= above2;
-    const uint32_t nc = min(ncand, (uint32_t)kListCandCap);
-    uint32_t cidx[kListCandPerThread], clow[kListCandPerThread];
-#pragma unroll
-    for (int i = 0; i < kListCandPerThread; ++i) {
-        const uint32_t j = (uint32_t)(tid + kSelThreads * i);
-        const uint2 c = j < nc ? cand[j] : make_uint2(0u, 0xffffffffu);
-        cidx[i] = c.x;
-        clow[i] = c.y;   // 0xffffffff: no candidate (above every 21-bit threshold, so tested first)
-    }
-    uint32_t sw;
-    if (n2 == krem) {
-        // bin d2 holds exactly the keys still to take: every candidate whose second digit is d2 or above
-#pragma unroll
-        for (int i = 0; i < kListCandPerThread; ++i)
-            if (clow[i] != 0xffffffffu && (clow[i] >> 10) >= d2) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
-        __syncthreads();
-        sw = bits[tid];
-    } else {
-#pragma unroll
-        for (int i = 0; i < kListCandPerThread; ++i)
-            if (clow[i] != 0xffffffffu && (clow[i] >> 10) == d2) atomicAdd(&hist3[clow[i] & 1023u], 1u);
-        __syncthreads();
-        find_digit_wave(sh, hist3, krem, 1024);
-        const uint32_t tlow = (d2 << 10) | (sh.digit & 1023u);
-        krem = sh.krem;
-        if (sh.dcount <= krem) {
-            // every key equal to the threshold is taken
-#pragma unroll
-            for (int i = 0; i < kListCandPerThread; ++i)
-                if (clow[i] != 0xffffffffu && clow[i] >= tlow) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
-            __syncthreads();
-            sw = bits[tid];
-        } else {
-            // ties at the threshold: the first krem of them in index order, ranked through the tie bitmap (thread t
-            // owns word t of both bitmaps after the scan's barriers)
-#pragma unroll
-            for (int i = 0; i < kListCandPerThread; ++i) {
-                if (clow[i] == 0xffffffffu) continue;
-                if (clow[i] > tlow) atomicOr(&bits[cidx[i] >> 5], 1u << (cidx[i] & 31u));
-                else if (clow[i] == tlow) atomicOr(&ties[cidx[i] >> 5], 1u << (cidx[i] & 31u));
-            }
-            __syncthreads();
-            uint32_t tw = ties[tid];
-            uint32_t rank, unused, tot, unused_t;
-            block_scan2<kSelThreads>((uint32_t)__popc(tw), 0u, rank, unused, tot, unused_t, sh.wave_tot);
-            sw = bits[tid];
-            while (tw && rank < krem) {
-                sw |= tw & (0u - tw);   // lowest set bit
-                tw &= tw - 1u;
-                ++rank;
-            }
-        }
-    }
-    init_sortbuf(a, sh);   // score order: the staged pairs' padding (the candidates in sortbuf are in registers now)
+    const ListLds L{sh.hist, lds, sup2, lds + 2048, lds + 3072, lds + 3072 + kListWords, hdr,
+                    reinterpret_cast<uint2*>(sh.sortbuf), misc, sh.wave_tot};
+    ListRow r;
+    r.srow = a.scores + (size_t)row * a.score_stride;
+    r.state = a.hist + (size_t)row * kSelectStateWords;
+    r.entries = t.entries + (size_t)row * t.tiles * t.cap;
+    r.hdr = t.hdr + (size_t)row * t.tiles;
+    r.M = a.M;
+    r.k = a.k;
+    r.lo = a.lo;
+    r.hi = a.hi;
+    r.cap = t.cap;
+    r.tiles = t.tiles;
+    r.nsub = t.nsub;
+    r.lspl = t.lspl;
+    list_select_bitmap<kSelThreads, kListSlots>(r, L);
+    const uint32_t sw = L.bits[threadIdx.x];
+    init_sortbuf(a, sh);   // score order: the staged pairs' padding (the candidates in sortbuf are no longer read)
     emit_word_row(a, row, sh, sw, block_excl_scan_once((uint32_t)__popc(sw), sh.wave_tot));
 }
 
@@ -1634,7 +1411,7 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
                     "the list select needs the select state and the lists");
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
-    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles)};
+    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots)};
     hipLaunchKernelGGL(select_lists, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
     return check_launch("select_lists");
 }

@@ -317,20 +317,26 @@ def test_list_select_on_hard_distributions(gpu, case, B, h, C, L, rho):
             check_out(out, ref, case)
 
 
-def test_list_select_state_is_left_clean(gpu):
-    """After steps through the list select (including a row that falls back to the streaming select), a step with
-    other shapes on the same select state is still bit-exact."""
+@pytest.mark.parametrize("canonical", [True, False])
+def test_list_select_state_is_left_clean(gpu, canonical):
+    """After steps through the list select (including a row resolved by passes over its scores), a step with other
+    shapes on the same select state is still bit-exact. Position order runs the fused select-and-attend (its
+    workgroups share the state, the last reader clears it; h = 4 at B = 2 splits each row over head groups), score
+    order the select kernel."""
     from attention_lab import decode as dec
-    for B, C, L, rho, case in ((1, 16384 + 64, 16384, 1 / 16, "all_equal"), (2, 8192 + 64, 8192, 1 / 8, None),
-                               (1, 2048 + 64, 2048, 1 / 32, None)):
-        K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=2, C=C, seed=C)
+    order = "position" if canonical else "score"
+    for B, h, C, L, rho, case in ((1, 2, 16384 + 64, 16384, 1 / 16, "all_equal"), (2, 4, 8192 + 64, 8192, 1 / 8, None),
+                                  (1, 2, 2048 + 64, 2048, 1 / 32, None)):
+        K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=C)
         req0 = prepare_request(B, 8, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
         lo, hi = req0.layout.candidate_lo, req0.layout.candidate_hi
         if case:
             _shape_scores(zT, lo, hi, case)
-        req, _, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, False)
+        req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical)
         s = kernel_scores(zT, q_pre, idx, lo, hi)
-        assert np.array_equal(pos, exact.select_rows(s, lo, hi, L, req.k, order="score"))
+        want = exact.select_rows(s, lo, hi, L, req.k, order=order)
+        assert np.array_equal(pos, want)
+        check_out(out, exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), want), f"{order} {B}x{L}")
         state = dec._STEP_WS.bytes(gpu, 0, "state")
         assert int(state.abs().sum()) == 0, "the select left its state dirty"
 
