@@ -97,7 +97,10 @@ def test_mfma_busy_fraction(tmp_path, capsys):
 
 
 def test_committed_profiles_feed_the_bench_line():
-    assert bench.measured_traffic() == pytest.approx(288_780_776, rel=1e-3)
+    """The committed score-kernel PMC summary gives the bench line's traffic: at least the algorithmic bytes of one
+    B=16, 32K launch (285,120,512) and within a few percent of them (the histogram atomics and the key lists)."""
+    traffic = bench.measured_traffic()
+    assert traffic is not None and 285_120_512 <= traffic <= 1.05 * 285_120_512
     assert 0.0 < bench.mfma_busy_from_profile() < 1.0
 
 
