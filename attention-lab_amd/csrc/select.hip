@@ -1164,8 +1164,17 @@ __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListAr
     __shared__ uint32_t misc[4];
     static_assert(kListCandCap * sizeof(uint2) <= sizeof(SelectShared::sortbuf), "candidates live in sortbuf");
     const int row = xcd_contiguous_block();   // the XCD whose score workgroups wrote the row
-    const ListLds L{sh.hist, lds, sup2, lds + 2048, lds + 3072, lds + 3072 + kListWords, hdr,
-                    reinterpret_cast<uint2*>(sh.sortbuf), misc, sh.wave_tot};
+    ListLds L;
+    L.hist = sh.hist;
+    L.hist2 = lds;
+    L.sup2 = sup2;
+    L.hist3 = lds + 2048;
+    L.bits = lds + 3072;
+    L.ties = lds + 3072 + kListWords;
+    L.hdr = hdr;
+    L.cand = reinterpret_cast<uint2*>(sh.sortbuf);
+    L.misc = misc;
+    L.wave_tot = sh.wave_tot;
     ListRow r;
     r.srow = a.scores + (size_t)row * a.score_stride;
     r.state = a.hist + (size_t)row * kSelectStateWords;

@@ -37,7 +37,8 @@ struct ListRow {
     int lspl;                 // log2 of the entries per lane and list loaded in the first round trip
 };
 
-// LDS of list_select_bitmap (the caller places the arrays, so that they can share memory with its other phases).
+// LDS of list_select_bitmap (the caller places the arrays, so that they can share memory with its other phases). Fill
+// it field by field in the kernel: an aggregate of LDS addresses given as a constant initializer cannot be emitted.
 struct ListLds {
     uint32_t* hist;           // kHistBins: the first digit's bins
     uint32_t* hist2;          // 2048: the second digit over bin b1
@@ -159,7 +160,7 @@ __device__ __forceinline__ void take_ties(const ListLds& L, uint32_t krem) {
 // Bin b1 too full for the candidate array: the remaining two digits by passes over the row's scores, then every key
 // above the threshold and the first krem keys equal to it. Called by every thread with the same b1 and krem.
 template <int THREADS>
-__device__ void radix_bitmap(const ListRow& r, const ListLds& L, uint32_t b1, uint32_t krem) {
+__device__ __forceinline__ void radix_bitmap(const ListRow& r, const ListLds& L, uint32_t b1, uint32_t krem) {
     constexpr int W = kListWords / THREADS;
     const int tid = threadIdx.x;
     const int M = r.M;
@@ -208,7 +209,7 @@ __device__ void radix_bitmap(const ListRow& r, const ListLds& L, uint32_t b1, ui
 // in the first round trip (the first 64 << r.lspl entries of each of the wave's first SLOTS >> r.lspl lists; later
 // entries and lists are read afterwards). Called by every thread of the workgroup.
 template <int THREADS, int SLOTS>
-__device__ void list_select_bitmap(const ListRow& r, const ListLds& L) {
+__device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListLds& L) {
     constexpr int kWaves = THREADS / 64;
     constexpr int W = kListWords / THREADS;
     static_assert(SLOTS % 8 == 0, "slots are taken in passes of 8");
