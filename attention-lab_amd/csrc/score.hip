@@ -817,7 +817,8 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
         // one launch: u and the z column inside the scan
         a.tiles = geo.tiles;
         const dim3 grid(BG * a.tiles), block(256);
-        if (geo.nsub == 4) hipLaunchKernelGGL(score_scan_fused<4>, grid, block, 0, s, a);
+        if (geo.nsub == 8) hipLaunchKernelGGL(score_scan_fused<8>, grid, block, 0, s, a);
+        else if (geo.nsub == 4) hipLaunchKernelGGL(score_scan_fused<4>, grid, block, 0, s, a);
         else if (geo.nsub == 2) hipLaunchKernelGGL(score_scan_fused<2>, grid, block, 0, s, a);
         else hipLaunchKernelGGL(score_scan_fused<1>, grid, block, 0, s, a);
         return check_launch("score_scan_fused");

@@ -1156,6 +1156,7 @@ struct ListArgs {
     int cap, tiles, nsub, lspl;
 };
 
+template <int MAXSUB>
 __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListArgs t) {
     __shared__ SelectShared sh;   // hist: the first digit's bins; sortbuf: candidates, then score order's pairs
     __shared__ __attribute__((aligned(16))) uint32_t lds[2048 + 1024 + 2 * kListWords];
@@ -1188,7 +1189,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListAr
     r.tiles = t.tiles;
     r.nsub = t.nsub;
     r.lspl = t.lspl;
-    list_select_bitmap<kSelThreads, kListSlots>(r, L);
+    list_select_bitmap<kSelThreads, kListSlots, MAXSUB>(r, L);
     const uint32_t sw = L.bits[threadIdx.x];
     init_sortbuf(a, sh);   // score order: the staged pairs' padding (the candidates in sortbuf are no longer read)
     emit_word_row(a, row, sh, sw, block_excl_scan_once((uint32_t)__popc(sw), sh.wave_tot));
@@ -1411,8 +1412,8 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
     int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride);
     if (rc) return rc;
     const int M = hi - lo;
-    ATTNLAB_REQUIRE(k > 0 && M <= kListMaxM && geo.nsub >= 1 && geo.tiles >= 1 && geo.tiles <= kListMaxTiles &&
-                        (int64_t)geo.tiles * geo.nsub * 512 >= ((hi + 7) & ~7) - (lo & ~7),
+    ATTNLAB_REQUIRE(k > 0 && M <= kListMaxM && geo.nsub >= 1 && geo.nsub <= 8 && geo.tiles >= 1 &&
+                        geo.tiles <= kListMaxTiles && (int64_t)geo.tiles * geo.nsub * 512 >= ((hi + 7) & ~7) - (lo & ~7),
                     "the list select needs 0 < k, M <= %d and the score tiling that wrote the lists", kListMaxM);
     ATTNLAB_REQUIRE(!staged_score_order(order, k), "the list select sorts at most %d rows in score order",
                     kMaxScoreOrderK);
@@ -1421,7 +1422,9 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
     ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots)};
-    hipLaunchKernelGGL(select_lists, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
+    // the instance for up to four sub-tiles per score workgroup keeps fewer registers live
+    if (geo.nsub <= 4) hipLaunchKernelGGL(select_lists<4>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
+    else hipLaunchKernelGGL(select_lists<8>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
     return check_launch("select_lists");
 }
 

@@ -207,9 +207,11 @@ __device__ __forceinline__ void radix_bitmap(const ListRow& r, const ListLds& L,
 
 // The selection bitmap of one row (in L.bits, complete and synchronised on return). SLOTS: entries per lane loaded
 // in the first round trip (the first 64 << r.lspl entries of each of the wave's first SLOTS >> r.lspl lists; later
-// entries and lists are read afterwards). Called by every thread of the workgroup.
-template <int THREADS, int SLOTS>
+// entries and lists are read afterwards). MAXSUB (4 or 8): the most sub-tiles per score workgroup this instance reads
+// for an incomplete list (r.nsub <= MAXSUB). Called by every thread of the workgroup.
+template <int THREADS, int SLOTS, int MAXSUB>
 __device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListLds& L) {
+    static_assert(MAXSUB == 4 || MAXSUB == 8, "sub-tiles are read four at a time");
     constexpr int kWaves = THREADS / 64;
     constexpr int W = kListWords / THREADS;
     static_assert(SLOTS % 8 == 0, "slots are taken in passes of 8");
@@ -322,29 +324,33 @@ __device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListL
                 take(idx, key, ok, 8);
             }
         } else {
-            // an incomplete list: the tile's scores, lane -> 8 consecutive columns of each sub-tile, every load issued
-            // before the first is used
+            // an incomplete list: the tile's scores, lane -> 8 consecutive columns of each sub-tile, four sub-tiles'
+            // loads issued before the first is used
             const int cb = (r.lo & ~7) + w * 512 + lane * 8;
-            float v[4][8];
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int sb = 0; sb < MAXSUB; sb += 4) {
+                if (sb >= r.nsub) break;
+                float v[4][8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int c = cb + s * nt * 512 + i;
-                    v[s][i] = s < r.nsub && c >= r.lo && c < r.hi ? r.srow[c - r.lo] : 0.0f;
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int c = cb + (sb + s) * nt * 512 + i;
+                        v[s][i] = sb + s < r.nsub && c >= r.lo && c < r.hi ? r.srow[c - r.lo] : 0.0f;
+                    }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    if (sb + s >= r.nsub) break;
+                    uint32_t idx[8], key[8], ok = 0u;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int c = cb + (sb + s) * nt * 512 + i;
+                        key[i] = score_key(v[s][i]);
+                        idx[i] = (uint32_t)(c - r.lo);
+                        ok |= (uint32_t)(c >= r.lo && c < r.hi) << i;
+                    }
+                    take(idx, key, ok, 8);
                 }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (s >= r.nsub) break;
-                uint32_t idx[8], key[8], ok = 0u;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int c = cb + s * nt * 512 + i;
-                    key[i] = score_key(v[s][i]);
-                    idx[i] = (uint32_t)(c - r.lo);
-                    ok |= (uint32_t)(c >= r.lo && c < r.hi) << i;
-                }
-                take(idx, key, ok, 8);
             }
         }
     }

@@ -86,8 +86,8 @@ def test_select_scratch_formula(native_lib):
 
 
 def list_region(BG, lo, hi, k):
-    """The score kernel's per-workgroup key lists: workgroups of 1, 2 or 4 sub-tiles of 512 columns (as many as keep
-    2048 workgroups in the grid), a list of at least lmin = s + 3 floor(sqrt(s)) + 16 keys for the even share
+    """The score kernel's per-workgroup key lists: workgroups of 8 sub-tiles of 512 columns where 1024 workgroups remain,
+    else 4, 2 or 1 (as many as keep 2048 workgroups in the grid), a list of at least lmin = s + 3 floor(sqrt(s)) + 16 keys for the even share
     s = ceil(k * n / M) of n keys per workgroup and at most cap = min(n, lmin + 192 rounded up to 64) entries of 8
     bytes, and an 8-byte header per workgroup. None where the list select does not apply (M > 32768, more than 128
     workgroups per row, 2 * lmin > n)."""
@@ -96,7 +96,7 @@ def list_region(BG, lo, hi, k):
         return 0
     span = ((hi + 7) & ~7) - (lo & ~7)
     blocks = BG * ((span + 511) // 512)
-    nsub = 4 if blocks >= 4 * 2048 else 2 if blocks >= 2 * 2048 else 1
+    nsub = 8 if blocks >= 8 * 1024 else 4 if blocks >= 4 * 2048 else 2 if blocks >= 2 * 2048 else 1
     n = 512 * nsub
     tiles = (span + n - 1) // n
     share = (k * n + M - 1) // M
@@ -116,11 +116,13 @@ def test_workspace_size_formula(native_lib):
         sel = a(max(select_scratch(BG, M, k, 1), list_region(BG, lo, hi, k))) if k > 0 else 0
         return scores + a(BG * S * 4) + u + sel + (a(BG * P * h * 130 * 4) if P > 1 else 0)
     for args in ((16, 8, 4, 4, 32704, 32768, 1024, 4), (1, 8, 2, 4, 1984, 2048, 64, 1), (2, 8, 2, 60, 60, 60, 0, 8),
-                 (16, 8, 2, 4, 32704, 32768, 2048, 1), (1, 8, 2, 4, 32704, 32768, 2048, 1),
+                 (16, 8, 2, 4, 32704, 32768, 2048, 1), (16, 8, 2, 4, 32704, 32768, 4096, 1),
+                 (1, 8, 2, 4, 32704, 32768, 2048, 1),
                  (1, 8, 2, 4, 32704, 32768, 16384, 1), (4, 8, 2, 4, 300, 364, 32, 1)):
         assert native_lib.attnlab_sparse_decode_workspace(*args) == expect(*args)
-    # the lists outgrow the tiled select's scratch at B = 16, 32K, k = 2048
-    assert list_region(128, 4, 32704, 2048) > select_scratch(128, 32700, 2048, 1)
+    # the lists outgrow the tiled select's scratch at B = 16, 32K, k = 4096, and not at k = 1024
+    assert list_region(128, 4, 32704, 4096) > select_scratch(128, 32700, 4096, 1)
+    assert 0 < list_region(128, 4, 32704, 1024) < select_scratch(128, 32700, 1024, 1)
 
 
 def test_list_bytes_formula(native_lib):
