@@ -224,7 +224,6 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
     __shared__ float u_sh[32];
     __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
     __shared__ __attribute__((aligned(16))) float part[4][kCols];
-    __shared__ uint32_t lcount[2];   // the key list: entries placed, waves done
     const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
     const int bg = lin / a.tiles;
     const int tile = lin - bg * a.tiles;
