@@ -119,12 +119,14 @@ int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, 
 struct FusedGeometry {
     int nsub, tiles;
 };
-// Sub-tiles per workgroup: 8 where that still leaves 1024 workgroups (4 per CU: each workgroup's tail, the histogram
-// flush and the key list, then runs half as often), else as many as keep at least 2048 workgroups (8 per CU).
+// Sub-tiles per workgroup: 8, 4 or 2, as many as still leave 1024 workgroups (each workgroup's tail, the histogram
+// flush and the key list, then runs as rarely as the chip's occupancy allows); small grids (B = 1 at 32K) take 2 while
+// 256 workgroups remain (one per CU: half as many lists for the select to read, the latency of one workgroup's chain
+// unchanged); else 1.
 inline FusedGeometry fused_tiling(int BG, int lo, int hi) {
     const int span = ((hi + 7) & ~7) - (lo & ~7);
     const int64_t blocks512 = (int64_t)BG * ((span + 511) / 512);
-    const int nsub = blocks512 >= 8 * 1024 ? 8 : blocks512 >= 4 * 2048 ? 4 : blocks512 >= 2 * 2048 ? 2 : 1;
+    const int nsub = blocks512 >= 8 * 1024 ? 8 : blocks512 >= 4 * 1024 ? 4 : blocks512 >= 2 * 256 ? 2 : 1;
     return FusedGeometry{nsub, (span + 512 * nsub - 1) / (512 * nsub)};
 }
 FusedGeometry fused_geometry(int BG, int C, int r, int hd, int lo, int hi, const void* zT, bool u_given);
