@@ -208,6 +208,76 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* buf, int n) {
     }
 }
 
+// Score order for up to 1024 staged pairs (one per thread): a stable LSD radix sort on the pair's key, four passes of
+// 8 bits, descending (each digit complemented). The pairs arrive in ascending index order (the emission's slots), so
+// stability leaves equal keys in index order, the same order as sorting on (key, ~index). A pass: the lanes of a wave
+// holding the same digit find each other with eight ballots (rank among them: the lanes below); each group's leader
+// writes its count into a [wave][digit] table; 256 threads turn each digit's column into exclusive prefixes over the
+// waves and a block scan over the digits gives each digit's first slot; every pair then moves to its slot in the other
+// buffer. Two count tables alternate, so the one for the next pass is cleared while this one is read: four barriers
+// per pass. Buffers: sortbuf[0, 1024) and sortbuf[1024, 2048); tables and digit bases in sh.hist and after the
+// buffers. Returns the buffer holding the sorted pairs.
+__device__ __forceinline__ const uint64_t* radix_sort_desc_1024(SelectShared& sh, int k) {
+    static_assert(sizeof(SelectShared::sortbuf) >= 3072 * sizeof(uint64_t) + 256 * sizeof(uint32_t),
+                  "two 1024-pair buffers, a count table and the digit bases after them");
+    static_assert(sizeof(SelectShared::hist) >= kSelWaves * 256 * sizeof(uint16_t), "one count table in hist");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = sort_len(k);
+    uint64_t* buf[2] = {sh.sortbuf, sh.sortbuf + 1024};
+    uint16_t (*cnt[2])[256] = {reinterpret_cast<uint16_t (*)[256]>(sh.hist),
+                               reinterpret_cast<uint16_t (*)[256]>(sh.sortbuf + 2048)};
+    uint32_t* dbase = reinterpret_cast<uint32_t*>(sh.sortbuf + 3072);
+    uint32_t* zero0 = reinterpret_cast<uint32_t*>(cnt[0]);
+    uint32_t* zero1 = reinterpret_cast<uint32_t*>(cnt[1]);
+    zero0[tid] = 0u;        // 16 x 256 uint16 = 2048 words per table, two per thread
+    zero0[tid + kSelThreads] = 0u;
+    __syncthreads();
+    const bool valid = tid < n;
+    const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        uint16_t (*c)[256] = cnt[pass & 1];
+        uint32_t* next = (pass & 1) ? zero0 : zero1;
+        const uint64_t x = valid ? buf[pass & 1][tid] : 0ull;
+        const uint32_t dg = 255u - ((uint32_t)(x >> (32 + 8 * pass)) & 255u);
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (dg >> b) & 1u;
+            const uint64_t m = __ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const uint32_t rank = (uint32_t)__popcll(peers & lt);
+        if (valid && rank == 0) c[wave][dg] = (uint16_t)__popcll(peers);
+        if (pass < 3) {   // the next pass's table, untouched in this one
+            next[tid] = 0u;
+            next[tid + kSelThreads] = 0u;
+        }
+        __syncthreads();
+        uint32_t total = 0u;
+        if (tid < 256) {   // digit tid: exclusive prefix over the waves, in place
+#pragma unroll
+            for (int w = 0; w < kSelWaves; ++w) {
+                const uint32_t v = c[w][tid];
+                c[w][tid] = (uint16_t)total;
+                total += v;
+            }
+        }
+        const uint32_t inc = wave_incl_scan(total);   // waves 0..3 hold the 256 digits
+        if (lane == 63 && wave < 4) sh.wave_tot[wave][0] = inc;
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t before = 0u;
+            for (int w = 0; w < wave; ++w) before += sh.wave_tot[w][0];
+            dbase[tid] = before + inc - total;
+        }
+        __syncthreads();
+        if (valid) buf[(pass + 1) & 1][dbase[dg] + c[wave][dg] + rank] = x;
+        __syncthreads();
+    }
+    return buf[0];   // four passes: back in the first buffer
+}
+
 // F positions and, in score order, the sorted candidates (the selected pairs are staged in sh.sortbuf).
 __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectShared& sh) {
     const int tid = threadIdx.x;
@@ -230,12 +300,14 @@ __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectS
     // descending on (key, ~index): larger score first, then lower index (sortbuf[0, sort_len(k)) was pre-filled by
     // init_sortbuf before the emission)
     __syncthreads();
-    bitonic_sort_desc(sh.sortbuf, sort_len(k));
+    const uint64_t* sorted = sh.sortbuf;
+    if (sort_len(k) <= kSelThreads) sorted = radix_sort_desc_1024(sh, k);
+    else bitonic_sort_desc(sh.sortbuf, sort_len(k));
     const float* srow = a.scores + (size_t)row * a.score_stride;
     int32_t* ti = a.top_idx ? a.top_idx + (size_t)row * a.top_stride : nullptr;
     float* tv = a.top_val ? a.top_val + (size_t)row * a.top_stride : nullptr;
     for (int j = tid; j < k; j += kSelThreads) {
-        const uint64_t e = sh.sortbuf[j];
+        const uint64_t e = sorted[j];
         // clamped: a slot left as padding (only possible with a histogram that does not match the scores) must
         // still name a position of this row
         const int idx = min(max((int)(0xffffffffu - (uint32_t)(e & 0xffffffffu)), 0), a.M - 1);
