@@ -208,74 +208,89 @@ __device__ __forceinline__ void bitonic_sort_desc(uint64_t* buf, int n) {
     }
 }
 
-// Score order for up to 1024 staged pairs (one per thread): a stable LSD radix sort on the pair's key, four passes of
-// 8 bits, descending (each digit complemented). The pairs arrive in ascending index order (the emission's slots), so
+// Score order for up to 1024 staged pairs (one per thread): a stable LSD radix sort on the pair's key, passes of 8
+// bits, descending (each digit complemented). The pairs arrive in ascending index order (the emission's slots), so
 // stability leaves equal keys in index order, the same order as sorting on (key, ~index). A pass: the lanes of a wave
 // holding the same digit find each other with eight ballots (rank among them: the lanes below); each group's leader
-// writes its count into a [wave][digit] table; 256 threads turn each digit's column into exclusive prefixes over the
-// waves and a block scan over the digits gives each digit's first slot; every pair then moves to its slot in the other
-// buffer. Two count tables alternate, so the one for the next pass is cleared while this one is read: four barriers
-// per pass. Buffers: sortbuf[0, 1024) and sortbuf[1024, 2048); tables and digit bases in sh.hist and after the
-// buffers. Returns the buffer holding the sorted pairs.
+// writes its count into a [digit][wave] table; one exclusive scan of the table's 4096 entries in that order (thread t
+// owns entries 4t..4t+3, one 8-byte read) gives every (digit, wave) group its first slot; every pair then moves to its
+// slot in the other buffer. Two count tables alternate, so the one for the next pass is cleared while this one is read:
+// four barriers per pass. A pass whose 8 bits are the same in every key would leave the order as it is and is skipped
+// (the bits that differ anywhere are gathered during the first pass). Buffers: sortbuf[0, 1024) and
+// sortbuf[1024, 2048); the tables after them. Returns the buffer holding the sorted pairs.
 __device__ __forceinline__ const uint64_t* radix_sort_desc_1024(SelectShared& sh, int k) {
-    static_assert(sizeof(SelectShared::sortbuf) >= 3072 * sizeof(uint64_t) + 256 * sizeof(uint32_t),
-                  "two 1024-pair buffers, a count table and the digit bases after them");
-    static_assert(sizeof(SelectShared::hist) >= kSelWaves * 256 * sizeof(uint16_t), "one count table in hist");
+    static_assert(sizeof(SelectShared::sortbuf) >= 4096 * sizeof(uint64_t),
+                  "two 1024-pair buffers and two count tables of 256 x 16 uint16");
+    static_assert(kSelThreads * 4 == 256 * kSelWaves, "four table entries per thread");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = sort_len(k);
-    uint64_t* buf[2] = {sh.sortbuf, sh.sortbuf + 1024};
-    uint16_t (*cnt[2])[256] = {reinterpret_cast<uint16_t (*)[256]>(sh.hist),
-                               reinterpret_cast<uint16_t (*)[256]>(sh.sortbuf + 2048)};
-    uint32_t* dbase = reinterpret_cast<uint32_t*>(sh.sortbuf + 3072);
-    uint32_t* zero0 = reinterpret_cast<uint32_t*>(cnt[0]);
-    uint32_t* zero1 = reinterpret_cast<uint32_t*>(cnt[1]);
-    zero0[tid] = 0u;        // 16 x 256 uint16 = 2048 words per table, two per thread
-    zero0[tid + kSelThreads] = 0u;
+    // pairs in sortbuf[1024 * cur, +1024), the pass's count table in sortbuf[2048 + 1024 * cur, +1024) as uint16
+    // [256][16]; cur alternates between passes (offsets, not an array of pointers, so the accesses stay LDS ones)
+    uint64_t* const base = sh.sortbuf;
+    reinterpret_cast<uint32_t*>(base + 2048)[tid] = 0u;   // table 0: 2048 words, two per thread
+    reinterpret_cast<uint32_t*>(base + 2048)[tid + kSelThreads] = 0u;
     __syncthreads();
     const bool valid = tid < n;
     const uint64_t lt = (1ull << lane) - 1ull;
+    uint32_t differ = 0xffffffffu;   // key bits that differ between some two pairs (all, until the first pass knows)
+    int cur = 0;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
-        uint16_t (*c)[256] = cnt[pass & 1];
-        uint32_t* next = (pass & 1) ? zero0 : zero1;
-        const uint64_t x = valid ? buf[pass & 1][tid] : 0ull;
-        const uint32_t dg = 255u - ((uint32_t)(x >> (32 + 8 * pass)) & 255u);
-        uint64_t peers = __ballot(valid);
+        if (pass > 0 && ((differ >> (8 * pass)) & 255u) == 0u) continue;   // uniform digit: a stable no-op
+        uint64_t* const src = base + 1024 * cur;
+        uint64_t* const dst = base + 1024 * (cur ^ 1);
+        uint16_t* const c = reinterpret_cast<uint16_t*>(base + 2048 + 1024 * cur);
+        uint32_t* const next = reinterpret_cast<uint32_t*>(base + 2048 + 1024 * (cur ^ 1));
+        const uint64_t x = valid ? src[tid] : 0ull;
+        const uint32_t key = (uint32_t)(x >> 32);
+        const uint32_t dg = 255u - ((key >> (8 * pass)) & 255u);
+        // lanes whose digit equals this lane's: per bit, the lanes that agree with it are the ballot of the bit
+        // XNOR this lane's bit as an all-ones / zero mask
+        const uint64_t act = __ballot(valid);
+        uint32_t plo = (uint32_t)act, phi = (uint32_t)(act >> 32);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            const bool bit = (dg >> b) & 1u;
-            const uint64_t m = __ballot(bit);
-            peers &= bit ? m : ~m;
+            const uint32_t bm = (uint32_t)__builtin_amdgcn_sbfe((int)key, 8 * pass + b, 1);   // 0 or ~0
+            const uint64_t m = __ballot(bm != 0u);
+            plo &= ~((uint32_t)m ^ bm);
+            phi &= ~((uint32_t)(m >> 32) ^ bm);
         }
+        const uint64_t peers = ((uint64_t)phi << 32) | plo;
         const uint32_t rank = (uint32_t)__popcll(peers & lt);
-        if (valid && rank == 0) c[wave][dg] = (uint16_t)__popcll(peers);
-        if (pass < 3) {   // the next pass's table, untouched in this one
-            next[tid] = 0u;
-            next[tid + kSelThreads] = 0u;
-        }
-        __syncthreads();
-        uint32_t total = 0u;
-        if (tid < 256) {   // digit tid: exclusive prefix over the waves, in place
+        const int slot = (int)dg * kSelWaves + wave;
+        if (valid && rank == 0) c[slot] = (uint16_t)__popcll(peers);
+        next[tid] = 0u;   // the next pass's table, untouched in this one
+        next[tid + kSelThreads] = 0u;
+        if (pass == 0) {   // OR over the block of key ^ (the first pair's key), a wave's share in wave_tot[.][1]
+            uint32_t d = valid ? key ^ (uint32_t)(base[0] >> 32) : 0u;
 #pragma unroll
-            for (int w = 0; w < kSelWaves; ++w) {
-                const uint32_t v = c[w][tid];
-                c[w][tid] = (uint16_t)total;
-                total += v;
-            }
-        }
-        const uint32_t inc = wave_incl_scan(total);   // waves 0..3 hold the 256 digits
-        if (lane == 63 && wave < 4) sh.wave_tot[wave][0] = inc;
-        __syncthreads();
-        if (tid < 256) {
-            uint32_t before = 0u;
-            for (int w = 0; w < wave; ++w) before += sh.wave_tot[w][0];
-            dbase[tid] = before + inc - total;
+            for (int m = 32; m >= 1; m >>= 1) d |= (uint32_t)__shfl_xor((int)d, m, 64);
+            if (lane == 0) sh.wave_tot[wave][1] = d;
         }
         __syncthreads();
-        if (valid) buf[(pass + 1) & 1][dbase[dg] + c[wave][dg] + rank] = x;
+        if (pass == 0) {
+            differ = 0u;
+#pragma unroll
+            for (int w = 0; w < kSelWaves; ++w) differ |= sh.wave_tot[w][1];
+        }
+        // exclusive scan of the table in (digit, wave) order: thread t owns entries 4t..4t+3
+        uint2* const cw = reinterpret_cast<uint2*>(c);
+        const uint2 raw = cw[tid];
+        const uint32_t c0 = raw.x & 0xffffu, c1 = raw.x >> 16, c2 = raw.y & 0xffffu, c3 = raw.y >> 16;
+        const uint32_t s = c0 + c1 + c2 + c3;
+        const uint32_t inc = wave_incl_scan(s);
+        if (lane == 63) sh.wave_tot[wave][0] = inc;
+        __syncthreads();
+        const uint32_t wt = (lane < wave) ? sh.wave_tot[lane][0] : 0u;   // lanes 0..14 of row 0: earlier waves
+        const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)row16_incl_scan(wt), 15);
+        const uint32_t e0 = before + inc - s, e1 = e0 + c0, e2 = e1 + c1, e3 = e2 + c2;
+        cw[tid] = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+        __syncthreads();
+        if (valid) dst[c[slot] + rank] = x;
+        cur ^= 1;
         __syncthreads();
     }
-    return buf[0];   // four passes: back in the first buffer
+    return base + 1024 * cur;
 }
 
 // F positions and, in score order, the sorted candidates (the selected pairs are staged in sh.sortbuf).
