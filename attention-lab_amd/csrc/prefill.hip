@@ -10,6 +10,9 @@
 // The kernel writes T*M*4 bytes and reads the keys once per 64-query tile (from L2 after the first), so at any T above
 // a few dozen it is bound by the score writes to HBM, not by the matrix cores: one 16x16x32 MFMA pair makes 16 x 16
 // dot products = 1 KB of scores at nh = 4 for 32 Kflop, which at 8 TB/s of writes asks for a quarter of the MFMA peak.
+// A workgroup stages its keys in LDS before its first MFMA, so its main loop issues stores and no global loads: on this
+// part loads and stores share one in-order completion counter, and a wait for a key load issued after a score store
+// would also wait for that store to reach memory.
 #include <type_traits>
 
 #include "common.h"
@@ -37,7 +40,14 @@ struct LightningBatchArgs {
 
 constexpr int kQTile = 64;     // queries per workgroup: 16 per wave
 constexpr int kKBlock = 64;    // keys per step of a wave: four 16-column MFMA tiles
-constexpr int kKTile = 1024;   // keys per workgroup
+constexpr int kKTile = 512;    // keys per workgroup, staged in LDS (32 KB)
+
+// LDS slot (16-byte units) of chunk kq (elements 8 kq .. 8 kq + 7) of key j of the workgroup's range: four keys share a
+// 256-byte row and the row's 16 slots are permuted by the row number, so the 16 lanes of one MFMA B read (keys
+// j0 + 4 n + c, n < 16, of a 64-key block, one chunk) land in 16 different slots, i.e. on all 64 banks once.
+__device__ __forceinline__ int key_slot(int j, int kq) {
+    return (j >> 2) * 16 + ((((j & 3) << 2) | kq) ^ ((j >> 2) & 15));
+}
 
 // 8 consecutive fp32 -> (head, remainder) 16-bit vectors, both rounded to nearest even.
 template <bool F16>
@@ -73,14 +83,14 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const std::conditional_t<F16, f1
     else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Workgroup = 64 queries x 1024 keys of one (b, kg); wave w owns queries [16 w, 16 w + 16) of the tile and walks the
+// Workgroup = 64 queries x 512 keys of one (b, kg); wave w owns queries [16 w, 16 w + 16) of the tile and walks the
 // keys 64 at a time. MFMA operands (lane l, n = l & 15, K elements 8 (l >> 4) .. + 7):
 //   A row n    = (query n / nh, head n % nh) of one row group of 16 / nh queries; the wave has nh such groups
 //   B column n = key m0 + 4 n + c for the c-th of four tiles, so after the four tiles a lane holds 4 adjacent keys
 //   D          lane l holds rows 4 (l >> 4) + i, i < 4, of column n
 // so every lane ends with whole heads of 4 / nh queries (nh = 8: half the heads, the other half in lane l ^ 16) and
-// writes them as one 16-byte store of 4 adjacent scores per query. The keys of the next step are loaded before the
-// current step's MFMAs.
+// writes them as one 16-byte store of 4 adjacent scores per query. The workgroup's keys (those its last visible query
+// reads, rounded up to whole blocks; past the table: its last key, results not stored) are staged in LDS first.
 template <bool F16, int NH, bool RELU>
 __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
     using vec8 = std::conditional_t<F16, f16x8_t, bf16x8_t>;
@@ -88,6 +98,7 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
     constexpr int NG = NH;                  // row groups per wave (16 queries)
     constexpr int QPL = NH >= 4 ? 1 : 4 / NH;   // queries per lane per row group
     constexpr int HPL = NH >= 4 ? 4 : NH;       // heads per lane per query
+    __shared__ u32x4_t ksh[kKTile * 4];
     const int lin = xcd_contiguous_block();   // a (b, kg)'s tiles on one XCD: its keys stay in that L2
     const int kt = lin % a.ktiles;
     const int rest = lin / a.ktiles;
@@ -97,20 +108,23 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int t_wave = qt * kQTile + wave * 16;
     const int m_begin = a.lo + kt * kKTile;
-    int m_end = min(a.hi, m_begin + kKTile);
-    if (a.q_pos0 >= 0) m_end = min(m_end, a.q_pos0 + min(t_wave + 15, a.T - 1) + 1);
-    if (t_wave >= a.T || m_begin >= m_end) return;   // whole wave: nothing of it is visible (no barrier below)
+    const bool causal = a.q_pos0 >= 0;
+    int m_wg = min(a.hi, m_begin + kKTile);   // keys read by the workgroup's last visible query
+    if (causal) m_wg = min(m_wg, a.q_pos0 + min(qt * kQTile + kQTile - 1, a.T - 1) + 1);
+    if (m_begin >= m_wg) return;   // the whole workgroup: nothing of it is visible (before the barrier)
 
     const int n = lane & 15, kq = lane >> 4;
     vec8 ahi[NG], alo[NG];
     float wv[NG][4];
     const float* qb = a.q + (size_t)bkg * a.T * NH * 32;
     const float* wb = a.w + (size_t)bkg * a.T * NH;
+    float4 qraw[NG][2];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         const int t = min(t_wave + g * QG + n / NH, a.T - 1);   // rows past T compute on the last query, not stored
         const float4* src = reinterpret_cast<const float4*>(qb + ((size_t)t * NH + n % NH) * 32 + 8 * kq);
-        split8<F16>(src[0], src[1], ahi[g], alo[g]);
+        qraw[g][0] = src[0];
+        qraw[g][1] = src[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int rr = 4 * kq + i;
@@ -118,17 +132,41 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
             wv[g][i] = wb[(size_t)tt * NH + rr % NH];
         }
     }
-
-    const uint16_t* kbase = a.keys + (size_t)bkg * a.Lk * 32 + 8 * kq;
-    auto load_keys = [&](int m0, vec8 (&b)[4]) {
+    // keys [m_begin, m_begin + nst) into LDS: all loads issued, then the stores (eight 16-byte chunks per thread)
+    {
+        const int nst = min(kKTile, (m_wg - m_begin + kKBlock - 1) / kKBlock * kKBlock);
+        const uint16_t* kb = a.keys + (size_t)bkg * a.Lk * 32;
+        u32x4_t kv[kKTile * 4 / 256];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int m = min(m0 + 4 * n + c, a.Lk - 1);   // past the range: a real key, result not stored
-            b[c] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4_t*>(kbase + (size_t)m * 32));
+        for (int i = 0; i < kKTile * 4 / 256; ++i) {
+            const int e = (int)threadIdx.x + 256 * i;
+            const int m = min(m_begin + min(e >> 2, nst - 1), a.Lk - 1);
+            kv[i] = *reinterpret_cast<const u32x4_t*>(kb + (size_t)m * 32 + 8 * (e & 3));
         }
+#pragma unroll
+        for (int i = 0; i < kKTile * 4 / 256; ++i) {
+            const int e = (int)threadIdx.x + 256 * i;
+            ksh[key_slot(e >> 2, e & 3)] = kv[i];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) split8<F16>(qraw[g][0], qraw[g][1], ahi[g], alo[g]);
+    __syncthreads();
+    int m_end = min(a.hi, m_begin + kKTile);
+    if (causal) m_end = min(m_end, a.q_pos0 + min(t_wave + 15, a.T - 1) + 1);
+    if (t_wave >= a.T || m_begin >= m_end) return;   // this wave: nothing visible (no barrier below)
+
+    // B tiles of the block at key offset j0 (a multiple of 64) from LDS: key j0 + 4 n + c, chunk kq, at slot
+    // 4 j0 + 16 n + ((4 c + kq) ^ n)
+    int boff[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) boff[c] = 16 * n + (((c << 2) | kq) ^ n);
+    auto read_keys = [&](int m0, vec8 (&b)[4]) {
+        const u32x4_t* kp = ksh + 4 * (m0 - m_begin);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) b[c] = __builtin_bit_cast(vec8, kp[boff[c]]);
     };
     float* ob = a.out + (size_t)bkg * a.T * a.out_stride - a.lo;
-    const bool causal = a.q_pos0 >= 0;
     // Scores of row group g against the four key tiles in b: v[p][c] = score of the lane's p-th query and key
     // m0 + 4 n + c (nh = 8: the sum over both lane halves' heads, in both lanes).
     auto scores = [&](int g, const vec8 (&b)[4], f32x4_t (&v)[QPL]) {
@@ -153,9 +191,8 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
     // nh = 8: the two lanes holding a query's halves store two scores each, so every lane stores
     const int half = NH == 8 ? 2 * (kq & 1) : 0;
 
-    // Interior blocks (every key visible to every query of the wave): unconditional stores, so the wait for the next
-    // block's keys counts exactly the stores issued after them. Then at most a couple of boundary blocks (the causal
-    // diagonal, the row end, queries past T) with per-score masks.
+    // Interior blocks (every key visible to every query of the wave): unconditional stores. Then at most a couple of
+    // boundary blocks (the causal diagonal, the row end, queries past T) with per-score masks.
     int m_int = m_begin;
     if (t_wave + 15 < a.T) {
         int lim = min(a.hi, m_begin + kKTile);
@@ -169,7 +206,10 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
 #pragma unroll
         for (int p = 0; p < QPL; ++p)
             rowp[g][p] = ob + (size_t)min(t_wave + g * QG + (4 * kq) / NH + p, a.T - 1) * a.out_stride + 4 * n + half;
-    auto store_block = [&](int m0, const vec8 (&b)[4]) {
+    int m0 = m_begin;
+    for (; m0 < m_int; m0 += kKBlock) {
+        vec8 b[4];
+        read_keys(m0, b);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             f32x4_t v[QPL];
@@ -185,30 +225,15 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
                 }
             }
         }
-    };
-    vec8 ka[4], kb[4];
-    load_keys(m_begin, ka);
-    int m0 = m_begin;
-    for (; m0 + kKBlock < m_int; m0 += 2 * kKBlock) {   // two blocks per trip: the buffers swap roles, no copies
-        load_keys(m0 + kKBlock, kb);
-        store_block(m0, ka);
-        load_keys(m0 + 2 * kKBlock, ka);
-        store_block(m0 + kKBlock, kb);
     }
-    if (m0 < m_int) {   // an odd interior block
-        load_keys(m0 + kKBlock, kb);
-        store_block(m0, ka);
-        m0 += kKBlock;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) ka[c] = kb[c];
-    }
-    vec8 (&cur)[4] = ka;
     for (; m0 < m_end; m0 += kKBlock) {
+        vec8 b[4];
+        read_keys(m0, b);
         const int mk = m0 + 4 * n;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             f32x4_t v[QPL];
-            scores(g, cur, v);
+            scores(g, b, v);
 #pragma unroll
             for (int p = 0; p < QPL; ++p) {
                 const int t = t_wave + g * QG + (4 * kq) / NH + p;
@@ -220,7 +245,6 @@ __global__ __launch_bounds__(256) void lightning_batched(LightningBatchArgs a) {
                     if (mk + c < limit) dst[c] = v[p][c];
             }
         }
-        load_keys(m0 + kKBlock, cur);
     }
 }
 
