@@ -50,9 +50,9 @@ extern "C" int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, 
 namespace {
 
 // The launches of one step after the argument checks; score(ws_u, scores, stride, state, lists) runs the score stage
-// for the index table's dtype. `geo` is the one-launch score's tiling when the score stage runs it (bf16 tables), else
-// nsub == 0; with it, and where list_plan applies, the score kernel also writes per-workgroup key lists and the list
-// select replaces the tiled select.
+// for the index table's dtype. `geo` is the one-launch score's tiling when the score stage runs it (bf16 or float32
+// tables), else nsub == 0; with it, and where list_plan applies, the score kernel also writes per-workgroup key lists
+// and the list select replaces the tiled select.
 template <typename Score>
 int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uint16_t* V, bool has_k_new, int B,
                             int G, int h, int C, int lo, int hi, int legal, int k, float scale, int order, int P,
@@ -135,11 +135,12 @@ extern "C" int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const floa
                                               int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream) {
     return sparse_decode_step_impl(
         q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
-        workspace_bytes, rows_out, rows_flat, out, stream, attnlab::FusedGeometry{0, 0},
-        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists*,
+        workspace_bytes, rows_out, rows_flat, out, stream,
+        attnlab::fused_geometry_f32(B * G, C, r, h * 128, lo, hi, zT, wq_t, false),
+        [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists* ls,
             hipStream_t s) {
             return attnlab::score_grouped_f32_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r,
-                                                   C, 128, h * 128, slo, shi, write_col, st, s);
+                                                   C, 128, h * 128, slo, shi, write_col, st, s, ls);
         });
 }
 

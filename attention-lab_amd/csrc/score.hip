@@ -421,37 +421,8 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         }
     }
     if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
-    if (a.lists.entries) {
-        // the list: every key of the tile whose first digit is at least that of the tile's lmin-th largest key (each
-        // wave finds that digit itself; the flush's barrier follows the last histogram update), in no particular
-        // order: a wave reserves its entries with one LDS atomic. The wave that finishes last writes the header.
-        const uint32_t dl = wave_digit_of_rank(hsh, (uint32_t)a.lists.lmin);
-        uint32_t m = 0u;
-#pragma unroll
-        for (int i = 0; i < 2 * NSUB; ++i) m |= (uint32_t)(((lvalid >> i) & 1u) && (lkey[i] >> kHistShift) >= dl) << i;
-        const uint32_t n = (uint32_t)__popc(m);
-        const uint32_t inc = wave_incl_scan(n);
-        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
-        uint32_t base = 0u;
-        if (lane == 0) base = atomicAdd(&lcount[0], tot);
-        uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)base, 0) + inc - n;
-        const int cap = a.lists.cap;
-        uint2* ent = a.lists.entries + ((size_t)bg * a.tiles + tile) * cap;
-#pragma unroll
-        for (int i = 0; i < 2 * NSUB; ++i) {
-            if ((m >> i) & 1u) {
-                const int c = cb0 + (i >> 1) * sstride + 2 * tid + (i & 1);
-                if (pos < (uint32_t)cap) ent[pos] = make_uint2((uint32_t)(c - lo), lkey[i]);
-                ++pos;
-            }
-        }
-        // acquire-release at workgroup scope: this wave's reservation is ordered before its "done", and the count read
-        // after the fourth wave's "done"
-        if (lane == 0 &&
-            __hip_atomic_fetch_add(&lcount[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP) == 256 / 64 - 1)
-            a.lists.hdr[(size_t)bg * a.tiles + tile] =
-                make_uint2(dl, __hip_atomic_load(&lcount[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    }
+    if (a.lists.entries)
+        write_key_list<NSUB>(a.lists, hsh, lcount, lkey, lvalid, (size_t)bg * a.tiles + tile, cb0, sstride, lo);
 }
 
 // 2-byte-load scan for tables whose rows are not 16-byte aligned: thread -> 8 adjacent columns from lo, never

@@ -4,9 +4,12 @@
 //   zT[b,g,j,write_col] = sum_e wk[g,j,e] * k_new[b,g,e]           (float32, stored unrounded)
 //   u[j]                = sum_f q_cat[b,g,f] * wq_t[g,f,j]          (1/sqrt(r) folded into wq_t, as in the reference)
 //   out[b,g,m]          = sum_j u[j] * zT[b,g,j,lo+m]               for m in [lo, hi)
-// Two launches: a prologue (u and the z column, one workgroup per (b, g)) and a scan that reads the table with
-// 16-byte loads (4 columns of one row per load) and leaves the first-digit histogram for the tiled select, as the
-// bf16 scan does. The table is 4 bytes per element, so the scan moves twice the bf16 bytes.
+// Where the bf16 path's one-launch tiling applies (r = 32, h*d <= 512, 16-byte rows), one launch does it all:
+// score_scan_fused_f32 computes u and the z column inside the scan and writes the first-digit histogram and the
+// per-workgroup key lists of the list select, exactly as the bf16 kernel does. Otherwise two launches: a prologue
+// (u and the z column, one workgroup per (b, g)) and a scan with 16-byte loads (4 columns of one row per load) that
+// leaves the first-digit histogram for the tiled select. The table is 4 bytes per element, so the scan moves twice
+// the bf16 bytes.
 #include "common.h"
 #include "select.h"
 
@@ -26,12 +29,30 @@ struct ScoreF32Args {
     int G, r, C, d, hd, lo, M, write_col;
     int tiles;
     uint32_t* hist;         // select state [BG, kSelectStateWords] or null
+    ScoreLists lists;       // per-workgroup key lists (entries null: none; score_scan_fused_f32 only)
 };
 
 typedef float f32x4v_t __attribute__((ext_vector_type(4)));
 
 constexpr int kF32MaxR = 32;
 constexpr int kF32Cols = 1024;   // columns per scan workgroup: 256 threads x 4
+
+// z column of the newest key, 256 threads: thread -> (j = tid / 8, e = tid % 8, +8, ...); the 8 partial sums of a j
+// are adjacent lanes (shuffle reduce).
+__device__ __forceinline__ void write_z_f32(const ScoreF32Args& a, int bg, int g) {
+    const int tid = threadIdx.x;
+    const int j = tid >> 3, e0 = tid & 7;
+    const float* kn = a.k_new + (size_t)bg * a.d;
+    float acc = 0.0f;
+    if (j < a.r) {
+        const float* wr = a.wk + ((size_t)g * a.r + j) * a.d;
+        for (int e = e0; e < a.d; e += 8) acc += wr[e] * kn[e];
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (j < a.r && e0 == 0) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = acc;
+}
 
 // u (and the z column), one workgroup per (b, g).
 // u: with r % 4 == 0 and 16-byte rows, thread -> (columns 4*(tid % 8) .. +3 of u, feature slice tid / 8 of 32): 16
@@ -86,19 +107,7 @@ __global__ __launch_bounds__(256) void score_prologue_f32(ScoreF32Args a) {
             }
         }
     }
-    if (a.k_new) {
-        const int j = tid >> 3, e0 = tid & 7;
-        const float* kn = a.k_new + (size_t)bg * a.d;
-        float acc = 0.0f;
-        if (j < a.r) {
-            const float* wr = a.wk + ((size_t)g * a.r + j) * a.d;
-            for (int e = e0; e < a.d; e += 8) acc += wr[e] * kn[e];
-        }
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
-        acc += __shfl_xor(acc, 4);
-        if (j < a.r && e0 == 0) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = acc;
-    }
+    if (a.k_new) write_z_f32(a, bg, g);
 }
 
 // Scan: thread -> 4 adjacent columns from a 4-aligned column, one 16-byte load per index row j (all r loads issued
@@ -157,6 +166,145 @@ __global__ __launch_bounds__(256) void score_scan_f32(ScoreF32Args a) {
         }
     }
     if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
+}
+
+// One launch per step over a float32 table, with the bf16 one-launch kernel's tiling and outputs (r = 32,
+// C % 8 == 0, 16-byte aligned table; for u: h*d <= 512, 16-byte aligned wq_t): u from q_cat and wq_t (or given, read
+// from u_in, for a scan in the same summation order), the z column (tile 0), the scan of
+// NSUB sub-tiles of 512 columns (sub-tile s of workgroup w is the row's sub-tile s * tiles + w: at each step the row's
+// workgroups read one contiguous stretch of every table row), the first-digit histogram and the key lists. Wave w
+// reads table rows 8w .. 8w + 7; lane l -> columns 4l .. 4l + 3 and 256 + 4l .. 256 + 4l + 3 of the sub-tile, so each
+// of its two 16-byte loads per row is one contiguous kilobyte across the wave (16 loads per sub-tile, double
+// buffered); the waves' partial sums meet in LDS and thread t finishes columns 2t and 2t + 1 of the sub-tile.
+template <int NSUB>
+__global__ __launch_bounds__(256) void score_scan_fused_f32(ScoreF32Args a) {
+    constexpr int kCols = 512;
+    constexpr int kUIter = 512 / 64;   // q_cat features per lane
+    __shared__ __attribute__((aligned(16))) uint32_t hsh[kHistBins];
+    __shared__ __attribute__((aligned(16))) float part[4][kCols];
+    __shared__ uint32_t lcount[2];   // the key list: entries placed, waves done
+    const int lin = xcd_contiguous_block();   // a row's tiles on one XCD, which also selects from the row
+    const int bg = lin / a.tiles;
+    const int tile = lin - bg * a.tiles;
+    const int g = bg % a.G;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lo = a.lo, hi = a.lo + a.M;
+    const int cb0 = (lo & ~7) + tile * kCols;
+    const int sstride = a.tiles * kCols;
+    const int c_last = (hi - 1) & ~3;   // last 4-column group holding a scanned column (in bounds: C % 8 == 0)
+    const float* zw = a.zT + ((size_t)bg * 32 + 8 * wave) * a.C;
+
+    // Sub-tile s: this lane's two 4-column groups of the wave's 8 table rows. Groups past the row end re-read the last
+    // group (in bounds, results discarded), so every sub-tile issues the same sixteen loads.
+    auto load = [&](int s, f32x4v_t (&v)[16]) {
+        const int ca = min(cb0 + s * sstride + lane * 4, c_last);
+        const int cb = min(cb0 + s * sstride + 256 + lane * 4, c_last);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const float* row = zw + (size_t)jj * a.C;
+            v[2 * jj] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v_t*>(row + ca));
+            v[2 * jj + 1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v_t*>(row + cb));
+        }
+    };
+    // u[8 wave + c], c < 8: lane -> features lane + 64 i (two 16-byte weight loads each). The weight loads are issued
+    // before the table loads, so u is built while the table is in flight. Features past hd re-read feature hd - 1
+    // with q = 0 (no branch, so no wait is placed between the loads).
+    float u[8];
+    f32x4v_t vb[2][16];
+    if (a.u_in) {   // u given: the same scan, so the scores match the one-launch form's bit for bit
+        const float* up = a.u_in + (size_t)bg * 32 + 8 * wave;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) u[c] = up[c];
+        load(0, vb[0]);
+    } else {
+        const float* qp = a.q_cat + (size_t)bg * a.hd;
+        const float* wp = a.wq_t + (size_t)g * a.hd * 32 + 8 * wave;
+        f32x4v_t wv[kUIter][2];
+        float qf[kUIter];
+#pragma unroll
+        for (int it = 0; it < kUIter; ++it) {
+            const int f = lane + 64 * it;
+            const int fc = min(f, a.hd - 1);
+            const f32x4v_t* wr = reinterpret_cast<const f32x4v_t*>(wp + (size_t)fc * 32);
+            wv[it][0] = wr[0];
+            wv[it][1] = wr[1];
+            qf[it] = qp[fc];
+            if (f >= a.hd) qf[it] = 0.0f;
+        }
+        load(0, vb[0]);
+        __builtin_amdgcn_sched_barrier(0);   // keep every load above the first use of a weight
+#pragma unroll
+        for (int c = 0; c < 8; ++c) u[c] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < kUIter; ++it)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) u[c] += qf[it] * wv[it][c >> 2][c & 3];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float x = sum8(u[c]);
+            x += dpp_f32<0x140>(x);   // row_mirror: lane i <-> 15 - i, so the two groups of 8 of each row meet
+            const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+            const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+            const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+            const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+            u[c] = (r0 + r1) + (r2 + r3);
+        }
+    }
+    if (a.hist) clear_histogram<256>(hsh);
+    if (tid < 2) lcount[tid] = 0u;
+    __syncthreads();
+
+    float* o = a.out + (size_t)bg * a.out_stride - lo;
+    uint32_t lkey[2 * NSUB];   // this thread's keys (columns cb0 + s * sstride + 2 tid + e), kept for the list
+    uint32_t lvalid = 0u;
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+        if (s + 1 < NSUB) load(s + 1, vb[(s + 1) & 1]);
+        const f32x4v_t (&v)[16] = vb[s & 1];
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += u[jj] * v[2 * jj + (i >> 2)][i & 3];
+        *reinterpret_cast<float4*>(&part[wave][lane * 4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4*>(&part[wave][256 + lane * 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        __syncthreads();
+        const int cc = 2 * tid;
+        const float2 p0 = *reinterpret_cast<const float2*>(&part[0][cc]);
+        const float2 p1 = *reinterpret_cast<const float2*>(&part[1][cc]);
+        const float2 p2 = *reinterpret_cast<const float2*>(&part[2][cc]);
+        const float2 p3 = *reinterpret_cast<const float2*>(&part[3][cc]);
+        const float s0 = (p0.x + p1.x) + (p2.x + p3.x), s1 = (p0.y + p1.y) + (p2.y + p3.y);
+        const int c = cb0 + s * sstride + cc;
+        lkey[2 * s] = score_key(s0);
+        lkey[2 * s + 1] = score_key(s1);
+        if (c >= lo && c < hi) {
+            o[c] = s0;
+            lvalid |= 1u << (2 * s);
+            if (a.hist) atomicAdd(&hsh[lkey[2 * s] >> kHistShift], 1u);
+        }
+        if (c + 1 >= lo && c + 1 < hi) {
+            o[c + 1] = s1;
+            lvalid |= 2u << (2 * s);
+            if (a.hist) atomicAdd(&hsh[lkey[2 * s + 1] >> kHistShift], 1u);
+        }
+        if (s + 1 < NSUB) __syncthreads();   // part is rewritten by the next sub-tile
+    }
+    if (tile == 0) {
+        if (a.k_new) write_z_f32(a, bg, g);
+        if (a.u_out && !a.u_in && lane < 8) {
+            float uo = u[0];
+#pragma unroll
+            for (int c = 1; c < 8; ++c) uo = lane == c ? u[c] : uo;
+            a.u_out[(size_t)bg * 32 + 8 * wave + lane] = uo;
+        }
+    }
+    if (a.hist) flush_histogram<256>(hsh, a.hist, bg);
+    if (a.lists.entries)
+        write_key_list<NSUB>(a.lists, hsh, lcount, lkey, lvalid, (size_t)bg * a.tiles + tile, cb0, sstride, lo);
 }
 
 // Bulk build: zT[bg, j, col0 + t] = wk[g, j, :] . k_pre[bg, t, :] in float32. Block = 4 waves over 64 positions;
@@ -275,9 +423,18 @@ __global__ __launch_bounds__(256) void project_keys_f32_mfma(ProjectF32Args a) {
 
 }  // namespace
 
+FusedGeometry fused_geometry_f32(int BG, int C, int r, int hd, int lo, int hi, const void* zT, const void* wq_t,
+                                 bool u_given) {
+    const bool table = C % 8 == 0 && reinterpret_cast<uintptr_t>(zT) % 16 == 0;
+    const bool u_ok = u_given || (hd >= 1 && hd <= 512 && reinterpret_cast<uintptr_t>(wq_t) % 16 == 0);
+    if (!table || !u_ok || r != 32 || hi <= lo) return FusedGeometry{0, 0};
+    return fused_tiling(BG, lo, hi);
+}
+
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,
                            const float* u_in, float* u_out, float* out, int64_t out_stride, int B, int G, int r,
-                           int C, int d, int hd, int lo, int hi, int write_col, uint32_t* hist, hipStream_t s) {
+                           int C, int d, int hd, int lo, int hi, int write_col, uint32_t* hist, hipStream_t s,
+                           const ScoreLists* lists) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
     ATTNLAB_REQUIRE(r >= 1 && r <= kF32MaxR, "index width r=%d outside [1, %d]", r, kF32MaxR);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= C, "need 0 <= lo <= hi <= C, got lo=%d hi=%d C=%d", lo, hi, C);
@@ -296,7 +453,26 @@ int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const
         ATTNLAB_REQUIRE(u_in || u_out, "give u_in, or q_cat, wq_t and a u_out buffer for the prologue");
     }
     const int BG = B * G;
-    ScoreF32Args a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 0, hist};
+    ScoreF32Args a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 0, hist,
+                   ScoreLists{nullptr, nullptr, 0, 0}};
+    // one launch (u or u given, z column, scan, histogram, key lists) wherever its tiling applies
+    const FusedGeometry geo = M > 0 ? fused_geometry_f32(BG, C, r, hd, lo, hi, zT, wq_t, u_in != nullptr)
+                                    : FusedGeometry{0, 0};
+    if (lists) {
+        ATTNLAB_REQUIRE(geo.nsub > 0 && hist != nullptr && lists->entries && lists->hdr && lists->lmin >= 1 &&
+                            lists->cap >= 1 && lists->cap <= 512 * geo.nsub,
+                        "key lists need the one-launch score (r = 32, h*d <= 512, aligned table) and a select state");
+        a.lists = *lists;
+    }
+    if (geo.nsub > 0) {
+        a.tiles = geo.tiles;
+        const dim3 grid(BG * a.tiles), block(256);
+        if (geo.nsub == 8) hipLaunchKernelGGL(score_scan_fused_f32<8>, grid, block, 0, s, a);
+        else if (geo.nsub == 4) hipLaunchKernelGGL(score_scan_fused_f32<4>, grid, block, 0, s, a);
+        else if (geo.nsub == 2) hipLaunchKernelGGL(score_scan_fused_f32<2>, grid, block, 0, s, a);
+        else hipLaunchKernelGGL(score_scan_fused_f32<1>, grid, block, 0, s, a);
+        return check_launch("score_scan_fused_f32");
+    }
     if (need_u || k_new) {
         ScoreF32Args p = a;
         if (!need_u) p.u_out = nullptr;

@@ -92,6 +92,42 @@ struct ScoreLists {
     int lmin, cap;
 };
 
+// The key list of one 256-thread score workgroup (list number `list`), called by every thread once the workgroup's
+// first-digit histogram in hsh is complete and synchronised: every valid key of its tile whose first digit is at least
+// that of the tile's lmin-th largest key (each wave finds that digit itself, no barrier), in no particular order. A
+// wave reserves its entries with one LDS atomic on lcount[0]; the wave that finishes last (lcount[1]) writes the
+// header. Both counters start at zero. Thread t's keys: lkey[i] of column cb0 + (i / 2) * sstride + 2 t + i % 2, valid
+// where bit i of lvalid is set.
+template <int NSUB>
+__device__ __forceinline__ void write_key_list(const ScoreLists& L, const uint32_t* hsh, uint32_t* lcount,
+                                               const uint32_t (&lkey)[2 * NSUB], uint32_t lvalid, size_t list,
+                                               int cb0, int sstride, int lo) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t dl = wave_digit_of_rank(hsh, (uint32_t)L.lmin);
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < 2 * NSUB; ++i) m |= (uint32_t)(((lvalid >> i) & 1u) && (lkey[i] >> kHistShift) >= dl) << i;
+    const uint32_t n = (uint32_t)__popc(m);
+    const uint32_t inc = wave_incl_scan(n);
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    uint32_t base = 0u;
+    if (lane == 0) base = atomicAdd(&lcount[0], tot);
+    uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)base, 0) + inc - n;
+    uint2* ent = L.entries + list * L.cap;
+#pragma unroll
+    for (int i = 0; i < 2 * NSUB; ++i) {
+        if ((m >> i) & 1u) {
+            const int c = cb0 + (i >> 1) * sstride + 2 * tid + (i & 1);
+            if (pos < (uint32_t)L.cap) ent[pos] = make_uint2((uint32_t)(c - lo), lkey[i]);
+            ++pos;
+        }
+    }
+    // acquire-release at workgroup scope: this wave's reservation is ordered before its "done", and the count read
+    // after the fourth wave's "done"
+    if (lane == 0 && __hip_atomic_fetch_add(&lcount[1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP) == 3)
+        L.hdr[list] = make_uint2(dl, __hip_atomic_load(&lcount[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
+
 // The argument checks of attnlab_select_rows (the decode step runs them before its first launch, so a rejected call
 // leaves the select state untouched).
 int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
@@ -181,6 +217,11 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
 // attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,
                            const float* u_in, float* u_out, float* out, int64_t out_stride, int B, int G, int r,
-                           int C, int d, int hd, int lo, int hi, int write_col, uint32_t* hist, hipStream_t stream);
+                           int C, int d, int hd, int lo, int hi, int write_col, uint32_t* hist, hipStream_t stream,
+                           const ScoreLists* lists = nullptr);
+// The float32 one-launch score's tiling (the bf16 kernel's, fused_tiling), or nsub == 0 where it does not apply:
+// r != 32, C % 8 != 0, zT not 16-byte aligned, an empty range, or (u not given) h*d > 512 or wq_t not 16-byte aligned.
+FusedGeometry fused_geometry_f32(int BG, int C, int r, int hd, int lo, int hi, const void* zT, const void* wq_t,
+                                 bool u_given);
 
 }  // namespace attnlab
