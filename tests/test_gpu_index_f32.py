@@ -155,6 +155,57 @@ def test_step_matches_oracle(gpu, B, h, C, L, rho, canonical):
     assert d.max() <= BF16_MAX and d.mean() <= BF16_MEAN, f"max {d.max():.3e} mean {d.mean():.3e}"
 
 
+def _shape_table(zT, lo, hi, case):
+    """Candidate columns [lo, hi) rearranged so the scores stress the list select (as for bf16 tables): one tile far
+    above the rest (its list is cut and the tile read in full), every score equal (one first-digit bin holds the row),
+    seven distinct values (ties at the threshold across every list). Scaling by powers of two is exact in fp32."""
+    M = hi - lo
+    if case == "skewed_tile":
+        zT[..., lo + M // 5: lo + M // 5 + 700] *= 4
+        zT[..., hi - 300: hi] *= 2
+    elif case == "all_equal":
+        zT[..., lo:hi] = zT[..., lo:lo + 1].expand(*zT.shape[:-1], M)
+    else:
+        src = lo + (torch.arange(M, device=zT.device) * 5) % 7
+        zT[..., lo:hi] = zT[..., src]
+
+
+@pytest.mark.parametrize("case", ["skewed_tile", "all_equal", "seven_values"])
+@pytest.mark.parametrize("B,h,C,L,rho", [
+    (2, 2, 8192 + 64, 8192, 1 / 8),       # one 512-column sub-tile per score workgroup, M < 8192
+    (1, 2, 16384 + 64, 16384, 1 / 16),    # M > 8192: an all-equal row overflows the select's LDS candidates
+    (16, 4, 16384, 16384, 1 / 32),        # two sub-tiles per score workgroup
+])
+def test_step_list_select_on_hard_distributions(gpu, case, B, h, C, L, rho):
+    """The float32 one-launch score's key lists through the list select, in both row orders, bit-exact against the
+    oracle's selection on the kernel's own scores."""
+    G = 8
+    zT, q_pre, k_pre_new, idx = setup(gpu, B, G, h, C, seed=L + B)
+    gen = torch.Generator().manual_seed(C)
+    K = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    q = torch.randn(B, G, h, 1, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    _shape_table(zT, lo, hi, case)
+    for canonical in (True, False):
+        z = zT.clone()
+        out, rows = sparse_decode_step_kernel(q, q_pre, K, V, z, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo,
+                                              lo, hi, req.k, req.selected_count, k_pre_new=k_pre_new,
+                                              write_col=req.write_col, return_rows=True, canonical_order=canonical)
+        u_out = torch.empty(B, G, 32, dtype=torch.float32, device=gpu)
+        s = hip_score.score_grouped(z, lo, hi, q_cat=q_pre.reshape(B, G, h * 128).contiguous(), wq_t=idx.wq_t_scaled,
+                                    u_out=u_out)
+        torch.cuda.synchronize()
+        pos = (rows.view(B, G, -1) - req.offsets).cpu().numpy()
+        want = exact.select_rows(s.cpu().numpy(), lo, hi, L, req.k, order="position" if canonical else "score")
+        assert np.array_equal(pos, want), f"{case} canonical={canonical}: row list differs from the oracle"
+        if canonical:
+            ref = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), want)
+            d = np.abs(f64(out).reshape(ref.shape) - ref)
+            assert d.max() <= BF16_MAX and d.mean() <= BF16_MEAN, f"{case}: max {d.max():.3e} mean {d.mean():.3e}"
+
+
 def test_step_validation(gpu):
     zT, q_pre, k_pre_new, idx = setup(gpu, 1, 8, 2, 300, seed=1)
     K = torch.zeros(1, 8, 300, 128, dtype=torch.bfloat16, device=gpu)
