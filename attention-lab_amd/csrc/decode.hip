@@ -78,6 +78,8 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     char* ws = static_cast<char*>(workspace);
     if (k == 0) state = nullptr;
+    // no row list leaves the call: its order shows only in the attend's summation order, so take the faster select
+    if (!rows_out && !rows_flat) order = ATTNLAB_ORDER_POSITION;
     float* scores = reinterpret_cast<float*>(ws + L.scores);
     int32_t* rows = rows_out ? rows_out : reinterpret_cast<int32_t*>(ws + L.rows);
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;

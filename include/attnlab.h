@@ -284,7 +284,9 @@ int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int
  * K/V: [B,G,C,128] bf16; zT: [B,G,r,C] bf16; wq_t: [G,h*128,r]; wk: [G,r,128]; k_new: [B,G,128] (nullable: the
  * z column is not written). F = [0, lo) U [hi, legal); k top candidates; write_col = legal - 1 for the reference's
  * plan. rows_out: [B*G, S] int32 positions (nullable: kept in the workspace); rows_flat: [B*G*S] int64 flat ids
- * (nullable). out: [B,G,h,128] bf16. P: split-K partitions of the attend (1..64). order as in attnlab_select_rows.
+ * (nullable). out: [B,G,h,128] bf16. P: split-K partitions of the attend (1..64). order as in attnlab_select_rows;
+ * with neither rows_out nor rows_flat given the row order is not observable (attention is the same over any order of
+ * its rows, up to the summation's rounding), and the step runs the position-order select, the faster one.
  * state: select state [B*G, ATTNLAB_SELECT_STATE_WORDS] uint32, zero before the first call; the score kernel fills
  * it and the select kernels clear it, so it stays zero between calls with no memset (the launches stay capturable in
  * a HIP graph). Nullable: the select kernel then runs its own first radix pass on one workgroup per row.
