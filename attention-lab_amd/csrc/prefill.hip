@@ -413,6 +413,14 @@ constexpr int kPaRows = 128;          // (query, head) rows per workgroup: 4 wav
 constexpr int kPaKeys = 64;           // keys per block
 constexpr int kPaKPitch = 128 + 8;    // bf16 per K row in LDS (272 bytes: 16-byte aligned rows)
 constexpr int kPaVPitch = 64 + 4;     // bf16 per V^T row in LDS (136 bytes)
+
+// V^T in LDS: row d (a head dim) holds the block's 64 keys as 16 groups of 4 (8 bytes); group g of row d sits at slot
+// g ^ ((d >> 4) & 7). The staging store of a wave writes 16 rows 8 apart, which without the permutation land on 4 of
+// the 32 banks (8-way conflicts); with it they cover all 32. The MFMA reads (32 consecutive rows, one group) keep one
+// permutation per 16 rows and stay conflict-free.
+__device__ __forceinline__ int vt_at(int d, int key) {
+    return d * kPaVPitch + ((((key >> 2) ^ (d >> 4)) & 15) << 2) + (key & 3);
+}
 constexpr float kPaLazy = 8.0f;       // rescale O only when the running max grows by more than 2^8
 
 // two fp32 -> packed bf16 pair, round to nearest even (gfx950 converts in hardware: v_cvt_pk_bf16_f32)
@@ -482,8 +490,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
             const uint32_t y[4] = {vr[u][1].x, vr[u][1].y, vr[u][1].z, vr[u][1].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {   // dims d0 + 2e, d0 + 2e + 1: (key 2kp, key 2kp + 1) pairs
-                *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * e) * kPaVPitch + 2 * kp]) = (x[e] & 0xffffu) | (y[e] << 16);
-                *reinterpret_cast<uint32_t*>(&vt[(d0 + 2 * e + 1) * kPaVPitch + 2 * kp]) = (x[e] >> 16) | (y[e] & 0xffff0000u);
+                *reinterpret_cast<uint32_t*>(&vt[vt_at(d0 + 2 * e, 2 * kp)]) = (x[e] & 0xffffu) | (y[e] << 16);
+                *reinterpret_cast<uint32_t*>(&vt[vt_at(d0 + 2 * e + 1, 2 * kp)]) = (x[e] >> 16) | (y[e] & 0xffff0000u);
             }
         }
     };
@@ -560,9 +568,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
             const int key0 = 32 * (ks2 >> 1) + 16 * (ks2 & 1) + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const uint16_t* vrow = &vt[(32 * dt + n) * kPaVPitch + key0];
-                const u32x2v_t lo4 = *reinterpret_cast<const u32x2v_t*>(vrow);
-                const u32x2v_t hi4 = *reinterpret_cast<const u32x2v_t*>(vrow + 8);
+                const u32x2v_t lo4 = *reinterpret_cast<const u32x2v_t*>(&vt[vt_at(32 * dt + n, key0)]);
+                const u32x2v_t hi4 = *reinterpret_cast<const u32x2v_t*>(&vt[vt_at(32 * dt + n, key0 + 8)]);
                 const bf16x8_t va = __builtin_bit_cast(bf16x8_t, u32x4_t{lo4.x, lo4.y, hi4.x, hi4.y});
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[ks2], o[dt], 0, 0, 0);
             }
