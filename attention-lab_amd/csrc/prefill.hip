@@ -13,6 +13,7 @@
 // A workgroup stages its keys in LDS before its first MFMA, so its main loop issues stores and no global loads: on this
 // part loads and stores share one in-order completion counter, and a wait for a key load issued after a score store
 // would also wait for that store to reach memory.
+#include <cfloat>
 #include <type_traits>
 
 #include "common.h"
@@ -497,6 +498,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
     };
 
     float m_run = -INFINITY, l_run = 0.0f;
+    // the scale (log2 domain), made positive: a negative scale flips the sign of q instead (exact in bf16), and a zero
+    // scale becomes the smallest normal float, which gives the same weights (every exponent below fp32's resolution)
+    // while a masked key's -inf * scale stays -inf instead of NaN
+    const float sc = a.scale_log2 == 0.0f ? FLT_MIN : fabsf(a.scale_log2);
+    if (a.scale_log2 < 0.0f) {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            qb[kk] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(u32x4_t, qb[kk]) ^ 0x80008000u);
+    }
     f32x16_t o[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -523,14 +533,16 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
                 s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[kk], s[kt], 0, 0, 0);
             }
         }
-        // this lane's scores: row R, keys kb + 32 kt + 8 (i / 4) + 4 g + i % 4
+        // this lane's scores: row R, keys kb + 32 kt + 8 (i / 4) + 4 g + i % 4. The scale is positive here (a negative
+        // one flipped the query's sign), so the block's largest scaled score comes from the raw scores and the scale
+        // costs one multiply per row here and rides in the exponent's FMA below.
         const bool full = kb + kPaKeys - 1 <= wave_first && kb + kPaKeys <= a.legal;   // no key of the block masked
         float bm = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float v = s[kt][i] * a.scale_log2;
+                float v = s[kt][i];
                 if (!full) {
                     const int key = kb + 32 * kt + 8 * (i >> 2) + 4 * g + (i & 3);
                     if (key > pos || key >= a.legal) v = -INFINITY;
@@ -538,7 +550,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
                 s[kt][i] = v;
                 bm = fmaxf(bm, v);
             }
-        bm = fmaxf(bm, shfl_xor_f32(bm, 32));
+        bm = fmaxf(bm, shfl_xor_f32(bm, 32)) * sc;
         if (bm > m_run + kPaLazy) {   // also the first block of the row (m_run = -inf)
             const float al = fast_exp2(m_run - bm);   // exp2(-inf) = 0
             l_run *= al;
@@ -549,15 +561,18 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
             m_run = bm;
         }
         // P^T (bf16) as the B operand of O^T += V^T P^T, one per 16-key step ks: tile ks / 2, accumulators
-        // 8 (ks % 2) .. + 7, i.e. keys 16 (ks % 2) + 4 g + {0..3, 8..11} of the tile
+        // 8 (ks % 2) .. + 7, i.e. keys 16 (ks % 2) + 4 g + {0..3, 8..11} of the tile. p = exp2(scale * s - m): one
+        // FMA and the exponential.
         bf16x8_t pb[4];
+        const float nm = -m_run;
 #pragma unroll
         for (int ks2 = 0; ks2 < 4; ++ks2) {
             uint32_t w4[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float p0 = m_run == -INFINITY ? 0.0f : fast_exp2(s[ks2 >> 1][8 * (ks2 & 1) + 2 * e] - m_run);
-                const float p1 = m_run == -INFINITY ? 0.0f : fast_exp2(s[ks2 >> 1][8 * (ks2 & 1) + 2 * e + 1] - m_run);
+                const float x0 = s[ks2 >> 1][8 * (ks2 & 1) + 2 * e], x1 = s[ks2 >> 1][8 * (ks2 & 1) + 2 * e + 1];
+                const float p0 = m_run == -INFINITY ? 0.0f : fast_exp2(fmaf(x0, sc, nm));
+                const float p1 = m_run == -INFINITY ? 0.0f : fast_exp2(fmaf(x1, sc, nm));
                 l_run += p0 + p1;
                 w4[e] = pack_bf16x2(p0, p1);
             }

@@ -51,6 +51,20 @@ def test_matches_the_oracle(gpu, h, T, p0, cut):
     check(out, want, f"h={h} T={T} p0={p0} legal={legal}")
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.09, 0.2])
+def test_scales_other_than_the_default(gpu, scale):
+    """A zero scale (uniform weights over the legal keys), a negative one (the kernel flips the query's sign and uses
+    |scale|) and a larger positive one, against the float64 oracle with the same scale; chunk edges and a cut."""
+    B, G, h, T, p0, cut = 2, 2, 4, 130, 61, 7
+    legal = p0 + T - cut
+    C = p0 + T + 11
+    K, V, q = inputs(gpu, B, G, h, T, C, seed=77)
+    out = hip_attend.prefill_attend(q, K, V, p0, legal, scale=scale)
+    torch.cuda.synchronize()
+    want = exact.causal_attention(f64(q), f64(K), f64(V), legal, list(range(p0, p0 + T)), scale=scale)
+    check(out, want, f"scale={scale}")
+
+
 def test_rows_past_valid_length_are_never_read(gpu):
     B, G, h, T, p0 = 1, 2, 2, 96, 40
     C = 200
