@@ -48,6 +48,7 @@ struct SelectShared {
     uint32_t wave_tot[kSelWaves][2];
     uint32_t digit, krem, dcount;
     uint64_t sortbuf[kMaxScoreOrderK];
+    uint32_t dbase[256];   // score order past 1024 picks: each digit's next slot in a radix pass
 };
 
 // Block-wide exclusive scan of two counters for THREADS (<= 1024) threads; tot_a / tot_b receive the block totals.
@@ -293,6 +294,112 @@ __device__ __forceinline__ const uint64_t* radix_sort_desc_1024(SelectShared& sh
     return base + 1024 * cur;
 }
 
+// Score order for 1024 < sort_len(k) <= 4096 staged pairs: the same stable LSD radix sort (passes of 8 bits, each
+// digit complemented so that ascending digit order is descending score; stability keeps equal keys in index order),
+// the pairs taken as up to four sub-blocks of 1024 (sub-block e: pairs 1024 e + t). A pass first counts its digit over
+// all pairs (LDS atomics) and scans the counts into each digit's first slot (dbase). Then, sub-block by sub-block in
+// order: the lanes of a wave holding the same digit find each other with eight ballots (rank among them: the lanes
+// below), each group's leader writes its count into a [digit][wave] table, a scan along each digit's row gives every
+// (digit, wave) group its offset among the sub-block's pairs of that digit, every pair moves to dbase + offset + rank,
+// and dbase advances by the sub-block's count of each digit. Passes whose 8 bits are the same in every key are
+// skipped. Buffers: sortbuf[0, 4096) and sortbuf[4096, 8192); the table in sh.hist. Returns the sorted buffer.
+__device__ __forceinline__ const uint64_t* radix_sort_desc_4096(SelectShared& sh, int k) {
+    static_assert(sizeof(SelectShared::sortbuf) >= 8192 * sizeof(uint64_t), "two 4096-pair buffers");
+    static_assert(sizeof(SelectShared::hist) >= 256 * kSelWaves * sizeof(uint16_t), "the count table in hist");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = sort_len(k);   // 2048 or 4096
+    const int E = n >> 10;
+    uint64_t* const base = sh.sortbuf;
+    uint16_t* const c = reinterpret_cast<uint16_t*>(sh.hist);   // [256][16]
+    uint32_t* const cw = sh.hist;
+    uint32_t* const db = sh.dbase;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    // key bits that differ between some two pairs: OR over the pairs of key ^ (the first pair's key)
+    {
+        const uint32_t k0 = (uint32_t)(base[0] >> 32);
+        uint32_t d = 0u;
+        for (int e = 0; e < E; ++e) d |= (uint32_t)(base[1024 * e + tid] >> 32) ^ k0;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) d |= (uint32_t)__shfl_xor((int)d, m, 64);
+        if (lane == 0) sh.wave_tot[wave][1] = d;
+    }
+    __syncthreads();
+    uint32_t differ = 0u;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) differ |= sh.wave_tot[w][1];
+    int cur = 0;
+    for (int pass = 0; pass < 4; ++pass) {
+        if (((differ >> (8 * pass)) & 255u) == 0u) continue;   // uniform digit: a stable no-op (the same in every wave)
+        const uint64_t* const src = base + 4096 * cur;
+        uint64_t* const dst = base + 4096 * (cur ^ 1);
+        const int sh8 = 32 + 8 * pass;
+        // phase 1: the digit's counts over all pairs, then their exclusive scan into db
+        __syncthreads();   // the previous pass's last table and db reads are done
+        if (tid < 256) db[tid] = 0u;
+        cw[tid] = 0u;
+        cw[tid + kSelThreads] = 0u;
+        __syncthreads();
+        for (int e = 0; e < E; ++e)
+            atomicAdd(&db[255u - ((uint32_t)(src[1024 * e + tid] >> sh8) & 255u)], 1u);
+        __syncthreads();
+        uint32_t v = 0u, inc = 0u;
+        if (tid < 256) {
+            v = db[tid];
+            inc = wave_incl_scan(v);
+            if (lane == 63) sh.wave_tot[wave][0] = inc;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t before = 0u;
+            for (int w = 0; w < wave; ++w) before += sh.wave_tot[w][0];
+            db[tid] = before + inc - v;
+        }
+        __syncthreads();
+        // phase 2: the sub-blocks in order
+        for (int e = 0; e < E; ++e) {
+            const uint64_t x = src[1024 * e + tid];
+            const uint32_t key = (uint32_t)(x >> 32);
+            const uint32_t dg = 255u - ((key >> (8 * pass)) & 255u);
+            uint32_t plo = 0xffffffffu, phi = 0xffffffffu;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint32_t bm = (uint32_t)__builtin_amdgcn_sbfe((int)key, 8 * pass + b, 1);   // 0 or ~0
+                const uint64_t m = __ballot(bm != 0u);
+                plo &= ~((uint32_t)m ^ bm);
+                phi &= ~((uint32_t)(m >> 32) ^ bm);
+            }
+            const uint64_t peers = ((uint64_t)phi << 32) | plo;
+            const uint32_t rank = (uint32_t)__popcll(peers & lt);
+            const int slot = (int)dg * kSelWaves + wave;
+            if (rank == 0) c[slot] = (uint16_t)__popcll(peers);
+            __syncthreads();
+            uint32_t rowtot = 0u;
+            if (tid < 256) {   // digit tid: exclusive prefix over the 16 waves' counts, in place
+                uint4* rp = reinterpret_cast<uint4*>(c + tid * kSelWaves);
+                uint4 r[2] = {rp[0], rp[1]};
+                uint32_t* w32 = reinterpret_cast<uint32_t*>(r);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t lo = w32[i] & 0xffffu, hi = w32[i] >> 16;
+                    w32[i] = rowtot | ((rowtot + lo) << 16);
+                    rowtot += lo + hi;
+                }
+                rp[0] = r[0];
+                rp[1] = r[1];
+            }
+            __syncthreads();
+            dst[db[dg] + c[slot] + rank] = x;
+            __syncthreads();
+            if (tid < 256) db[tid] += rowtot;   // the next sub-block's pairs of each digit follow these
+            cw[tid] = 0u;
+            cw[tid + kSelThreads] = 0u;
+            __syncthreads();
+        }
+        cur ^= 1;
+    }
+    return base + 4096 * cur;
+}
+
 // F positions and, in score order, the sorted candidates (the selected pairs are staged in sh.sortbuf).
 __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectShared& sh) {
     const int tid = threadIdx.x;
@@ -317,6 +424,7 @@ __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectS
     __syncthreads();
     const uint64_t* sorted = sh.sortbuf;
     if (sort_len(k) <= kSelThreads) sorted = radix_sort_desc_1024(sh, k);
+    else if (sort_len(k) <= 4 * kSelThreads) sorted = radix_sort_desc_4096(sh, k);
     else bitonic_sort_desc(sh.sortbuf, sort_len(k));
     const float* srow = a.scores + (size_t)row * a.score_stride;
     int32_t* ti = a.top_idx ? a.top_idx + (size_t)row * a.top_stride : nullptr;

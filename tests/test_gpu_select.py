@@ -63,6 +63,18 @@ def test_score_order_beyond_4096(gpu, M, k):
     check_topk(gpu, heavy_tail(2, M, seed=k), k)
 
 
+@pytest.mark.parametrize("M,k,gen", [(5000, 1025, "ties"), (9000, 2049, "specials"), (40000, 4096, "ties"),
+                                     (3000, 2048, "zeros"), (70000, 3000, "normal")])
+def test_score_order_sorts_of_two_to_four_thousand(gpu, M, k, gen):
+    """Score order with 1024 < k <= 4096: the LDS radix sort over two to four sub-blocks of 1024 pairs (digit counts,
+    then per sub-block offsets); ties stay in index order, NaN last, -0.0 == +0.0."""
+    rng = np.random.default_rng(M + k)
+    R = 3
+    s = {"normal": lambda: heavy_tail(R, M, seed=k), "ties": lambda: tie_heavy(rng, (R, M)),
+         "specials": lambda: specials(rng, (R, M)), "zeros": lambda: np.zeros((R, M), np.float32)}[gen]()
+    check_topk(gpu, s, k)
+
+
 @pytest.mark.parametrize("M,k,gen", [(32700, 16384, "normal"), (40000, 20000, "normal"), (32768, 32768, "normal"),
                                      (20000, 9000, "ties"), (12000, 10000, "specials"), (10000, 9000, "zeros"),
                                      (300000, 9000, "normal")])
