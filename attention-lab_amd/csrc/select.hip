@@ -455,18 +455,49 @@ struct Emitter {
     int64_t base;
     uint64_t* sortbuf;
 
-    __device__ __forceinline__ void put(uint32_t slot, int idx, uint32_t key) const {
+    // v: the key's score (read only in score order and for top_val)
+    __device__ __forceinline__ void put(uint32_t slot, int idx, float v) const {
         if (slot >= k) return;
         if (order == ATTNLAB_ORDER_SCORE) {
-            sortbuf[slot] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+            sortbuf[slot] = ((uint64_t)score_key(v) << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
             return;
         }
         if (ti) ti[slot] = idx;
-        if (tv) tv[slot] = srow[idx];
+        if (tv) tv[slot] = v;
         if (rows) rows[slot] = lo + idx;
         if (flat) flat[slot] = base + lo + idx;
     }
+
+    // The set bits of `word`, ascending, as indices idx0 + bit at slots slot, slot + 1, ...: the scores of up to eight
+    // of them are loaded before any is used, so a word costs one memory round trip per eight keys, not one per key.
+    __device__ __forceinline__ void put_word(uint32_t word, int idx0, uint32_t& slot) const {
+        const bool need = order == ATTNLAB_ORDER_SCORE || tv != nullptr;
+        while (word) {
+            int ix[8];
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ix[u] = word ? idx0 + (int)(__ffs(word) - 1) : -1;
+                word &= word - 1u;   // stays 0 once empty
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = (need && ix[u] >= 0) ? srow[ix[u]] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (ix[u] >= 0) put(slot++, ix[u], v[u]);
+        }
+    }
 };
+
+// The lowest n set bits of w (the tie rule: the first n keys equal to the threshold, in index order).
+__device__ __forceinline__ uint32_t lowest_bits(uint32_t w, uint32_t n) {
+    uint32_t keep = 0u;
+    for (; n != 0u && w != 0u; --n) {
+        keep |= w & (0u - w);
+        w &= w - 1u;
+    }
+    return keep;
+}
 
 __device__ __forceinline__ Emitter make_emitter(const SelectArgs& a, int row, SelectShared& sh) {
     Emitter e;
@@ -607,34 +638,27 @@ __global__ __launch_bounds__(kSelThreads) void select_reg(SelectArgs a) {
         const uint32_t gw = mine ? gtbits[tid] : 0u, ew = mine ? eqbits[tid] : 0u;
         uint32_t egt, eeq;
         block_excl_scan2(__popc(gw), __popc(ew), egt, eeq, sh);
-        uint32_t word = gw | ew;
+        uint32_t word = gw | lowest_bits(ew, krem > eeq ? krem - eeq : 0u);
         if (word) {
             uint32_t slot = egt + min(eeq, krem);
-            uint32_t ties = eeq;
             const bool direct = a.order == ATTNLAB_ORDER_POSITION && !a.top_idx && !a.top_val;
-            const int S = a.lo + (a.legal - a.hi) + a.k;
-            int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride + a.lo : nullptr;
-            int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S + a.lo : nullptr;
-            const int64_t base = (int64_t)row * a.C + a.lo;
-            const Emitter em = make_emitter(a, row, sh);
-            while (word) {
-                const uint32_t b = __ffs(word) - 1;
-                word &= word - 1;
-                const bool eq = (ew >> b) & 1u;
-                const bool take = !eq || ties < krem;
-                ties += eq;
-                if (!take) continue;
-                const int idx = 32 * tid + (int)b;
-                if (direct) {
-                    // the decode step's row list: candidate m at slot lo + (its rank), as the Emitter would write it
+            if (direct) {
+                // the decode step's row list: candidate m at slot lo + (its rank), as the Emitter would write it
+                const int S = a.lo + (a.legal - a.hi) + a.k;
+                int32_t* rows = a.rows ? a.rows + (size_t)row * a.rows_stride + a.lo : nullptr;
+                int64_t* flat = a.rows_flat ? a.rows_flat + (size_t)row * S + a.lo : nullptr;
+                const int64_t base = (int64_t)row * a.C + a.lo;
+                while (word) {
+                    const int idx = 32 * tid + (int)(__ffs(word) - 1);
+                    word &= word - 1;
                     if (slot < (uint32_t)a.k) {
                         if (rows) rows[slot] = a.lo + idx;
                         if (flat) flat[slot] = base + idx;
                     }
-                } else {
-                    em.put(slot, idx, score_key(s[idx]));
+                    ++slot;
                 }
-                ++slot;
+            } else {
+                make_emitter(a, row, sh).put_word(word, 32 * tid, slot);
             }
         }
     }
@@ -775,27 +799,22 @@ __device__ void select_row_streaming(const SelectArgs& a, int row, SelectShared&
             const uint32_t gw = L.gtbits[tid], ew = L.eqbits[tid];
             uint32_t egt, eeq, tgt, teq;
             block_scan2<kSelThreads>(__popc(gw), __popc(ew), egt, eeq, tgt, teq, sh.wave_tot);
-            uint32_t word = gw | ew;
+            const uint32_t ties = eq_before + eeq;   // tied keys before this thread's word
+            uint32_t word = gw | lowest_bits(ew, krem > ties ? krem - ties : 0u);
             if (word) {
-                uint32_t ties = eq_before + eeq;
                 uint32_t slot = gt_before + egt + min(ties, krem);
-                while (word) {
-                    const uint32_t b = __ffs(word) - 1;
-                    word &= word - 1;
-                    const bool eq = (ew >> b) & 1u;
-                    const bool take = !eq || ties < krem;
-                    ties += eq;
-                    if (!take) continue;
-                    const int idx = 4096 * c_w + 32 * tid + (int)b;
-                    if (direct) {
+                if (direct) {
+                    while (word) {
+                        const int idx = 4096 * c_w + 32 * tid + (int)(__ffs(word) - 1);
+                        word &= word - 1;
                         if (slot < (uint32_t)a.k) {
                             if (rows) rows[slot] = a.lo + idx;
                             if (flat) flat[slot] = base + idx;
                         }
-                    } else {
-                        em.put(slot, idx, score_key(s[idx]));
+                        ++slot;
                     }
-                    ++slot;
+                } else {
+                    em.put_word(word, 4096 * c_w + 32 * tid, slot);
                 }
             }
             gt_before += tgt;
@@ -1093,17 +1112,8 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
         return;
     }
     const Emitter em = make_emitter(a, row, sh);
-    const bool by_score = a.order == ATTNLAB_ORDER_SCORE;
 #pragma unroll
-    for (int j = 0; j < kMaxWordsPerThread; ++j) {
-        uint32_t word = sw[j];
-        while (word) {
-            const uint32_t b = __ffs(word) - 1;
-            word &= word - 1;
-            const int idx = (w0 + j) * 32 + (int)b;
-            em.put(slot++, idx, by_score ? score_key(srow[idx]) : 0u);
-        }
-    }
+    for (int j = 0; j < kMaxWordsPerThread; ++j) em.put_word(sw[j], (w0 + j) * 32, slot);
     for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
@@ -1224,15 +1234,7 @@ __device__ __forceinline__ void emit_word_row(const SelectArgs& a, int row, Sele
         for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
         return;
     }
-    const Emitter em = make_emitter(a, row, sh);
-    const bool by_score = a.order == ATTNLAB_ORDER_SCORE;
-    const float* srow = a.scores + (size_t)row * a.score_stride;
-    while (word) {
-        const uint32_t b = __ffs(word) - 1;
-        word &= word - 1;
-        const int idx = tid * 32 + (int)b;
-        em.put(slot++, idx, by_score ? score_key(srow[idx]) : 0u);
-    }
+    make_emitter(a, row, sh).put_word(word, tid * 32, slot);
     for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
