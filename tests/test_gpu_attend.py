@@ -306,6 +306,28 @@ def test_paged_cache_reads_exactly_what_the_contiguous_cache_reads(gpu, page, P,
     assert torch.isfinite(got).all() and np.abs(got.double().cpu().numpy() - ref2).max() <= TOL["out_atol"]
 
 
+@pytest.mark.parametrize("page,C,L,listed", [(1, 5000, 4900, True), (2, 12000, 11000, False), (4, 12000, 11000, False),
+                                           (8, 40000, 33000, True)])
+def test_paged_long_block_tables_and_several_chunks(gpu, page, C, L, listed):
+    """Block tables of up to 40000 / 8 = 5000 pages (page size 1 included) and the dense read of S > 4096 positions
+    (several chunks of staged positions, each translated after its own barrier) agree bit for bit with the contiguous
+    read."""
+    G, B, h = 8, 1, 2
+    K4, V4, q5 = make(gpu, G=G, h=h, C=C, seed=page + C, B=B)
+    q = q5[:, :, :, 0].contiguous()
+    kp, vp, bt = hip_attend.page_cache(K4, V4, page, spare_pages=3, generator=torch.Generator().manual_seed(C))
+    if listed:
+        rows = row_list(G, C, L, 1 / 16, seed=page, B=B)[0].to(torch.int32).to(gpu).contiguous()
+        flat = hip_attend.attend(q, K4, V4, rows, partitions=4, out_dtype=torch.float32)
+        got = hip_attend.attend_paged(q, kp, vp, bt, rows, partitions=4, out_dtype=torch.float32)
+    else:
+        rows_all = torch.arange(L, dtype=torch.int32, device=gpu).expand(B, G, L).contiguous()
+        flat = hip_attend.attend(q, K4, V4, rows_all, partitions=2, out_dtype=torch.float32)
+        got = hip_attend.attend_paged(q, kp, vp, bt, None, length=L, partitions=2, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, flat), "paged and contiguous reads differ"
+
+
 @pytest.mark.parametrize("page,L", [(16, 2048), (128, 1000)])
 def test_dense_read_of_a_paged_cache(gpu, page, L):
     """rows=None reads positions [0, L) of each sequence through its block table: the dense control over pages."""
