@@ -18,6 +18,8 @@ from . import _native as nat
 LDS_SORT_K = nat.LDS_SORT_K   # score order up to this k is sorted in LDS; past it, by a radix pass (tiled entry)
 TILED_MIN_M = 32768     # rows at least this long are selected by the tiled kernels (attnlab_topk_tiled)
 TILED_MAX_M = 262144    # ... and at most this long (longer rows take the single-workgroup select)
+REG_MAX_M = 32768       # rows up to this long fit the single-workgroup select's registers ...
+REG_MIN_ROWS = 128      # ... which beats the tiled kernels from this many rows on (the rows alone fill half the chip)
 ORDERS = {"position": nat.ORDER_POSITION, "score": nat.ORDER_SCORE}
 _WS = nat.Workspace()   # select state (zeroed once, left zeroed by every call) and scratch, per device
 
@@ -28,13 +30,21 @@ def _order_code(order) -> int:
     return ORDERS[order]
 
 
+def use_tiled(R: int, M: int) -> bool:
+    """The automatic choice of topk for R rows of M scores: the tiled kernels for rows of TILED_MIN_M..TILED_MAX_M
+    scores, except rows of at most REG_MAX_M scores when there are REG_MIN_ROWS or more of them (one workgroup per
+    row, keys in registers). Measured on MI355X at k = M/32, score order: 32K keys, 64 rows: 22.4 us tiled against
+    23.8; 256 rows: 33.3 against 27.6; 64K keys, 256 rows: 61.8 tiled against 66.3."""
+    return TILED_MIN_M <= M <= TILED_MAX_M and not (M <= REG_MAX_M and R >= REG_MIN_ROWS)
+
+
 def topk(scores, k: int, *, order: str = "score", tiled=None):
     """Top-k over the last dim of fp32 `scores` [..., M] -> (values fp32 [..., k], indices int64 [..., k]).
 
     order="score": descending score, ties lowest index first (torch.topk's sorted order with ties defined);
-    order="position": the same set, indices ascending. tiled: None picks the tiled kernels for rows of
-    TILED_MIN_M..TILED_MAX_M scores (and for score order past LDS_SORT_K, which needs their scratch), True / False
-    forces the choice where both apply (same result either way).
+    order="position": the same set, indices ascending. tiled: None picks by use_tiled (and the tiled kernels for
+    score order past LDS_SORT_K, which needs their scratch), True / False forces the choice where both apply (same
+    result either way).
     """
     if scores.dtype != torch.float32 or not scores.is_cuda:
         raise ValueError("scores must be a float32 tensor on a HIP device")
@@ -53,7 +63,7 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
     idx = torch.empty(R, max(k, 1), dtype=torch.int32, device=scores.device)
     val = torch.empty(R, max(k, 1), dtype=torch.float32, device=scores.device)
     if tiled is None:
-        tiled = TILED_MIN_M <= M <= TILED_MAX_M
+        tiled = use_tiled(R, M)
     if code == nat.ORDER_SCORE and k > LDS_SORT_K:
         tiled = True   # the radix pass of a long score order runs in the tiled entry's scratch
     if R and k and tiled:

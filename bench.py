@@ -598,7 +598,7 @@ def sweep_lightning_topk(torch, dev, emit):
                 state = torch.zeros(B * KG, nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
                 nbytes = nat.lib().attnlab_select_scratch_bytes(B * KG, L, k, nat.ORDER_SCORE)
                 scratch = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
-                tiled = hip_select.TILED_MIN_M <= L <= hip_select.TILED_MAX_M
+                tiled = hip_select.use_tiled(B * KG, L)
 
                 def select(i):
                     if tiled:

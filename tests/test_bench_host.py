@@ -131,3 +131,14 @@ def test_cpu_info_and_the_lightning_cpu_leg():
     s = exact.lightning_scores(keys.double().numpy()[None], q.double().numpy()[None], w.double().numpy()[None], 0, 500)[0]
     np.testing.assert_allclose(vals.numpy(), np.take_along_axis(s, idx.numpy(), -1), rtol=1e-5, atol=1e-5)
     assert np.array_equal(np.sort(idx.numpy(), -1), np.sort(exact.topk(s.astype(np.float32), 16), -1))
+
+
+def test_topk_picks_the_tiled_kernels_by_row_length_and_count():
+    """hip_select.topk's automatic choice (also the configs[1] sweep's): tiled kernels for 32K..256K keys, except rows
+    of at most 32K keys when 128 or more of them fill half the chip as one workgroup each."""
+    from attention_lab import hip_select
+    assert not hip_select.use_tiled(1, 16384)
+    assert hip_select.use_tiled(1, 32768) and hip_select.use_tiled(64, 32768)
+    assert not hip_select.use_tiled(128, 32768) and not hip_select.use_tiled(256, 32768)
+    assert hip_select.use_tiled(256, 65536) and hip_select.use_tiled(512, 262144)
+    assert not hip_select.use_tiled(1, 262145)
