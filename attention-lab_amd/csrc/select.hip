@@ -294,6 +294,95 @@ __device__ __forceinline__ const uint64_t* radix_sort_desc_1024(SelectShared& sh
     return base + 1024 * cur;
 }
 
+// Score order for k <= 1024 staged pairs in slots [0, k) (one per thread), when the keys spread out: one pass into
+// 2048 bins that are linear in the key over [kmin, kmax] (bin = (kmax - key) >> s, with s the smallest shift that
+// leaves at most 2048 bins, so bin order is descending key order), then each pair's rank inside its bin by comparison
+// with the bin's other pairs, larger (key, ~index) first (equal pairs, which only zero padding can form, by their
+// place in the bin). Six barriers in all, against four per pass of the radix sort. The top k of a smooth score
+// distribution puts a few pairs in a bin; when a bin holds more than kBinSortMax (ties, outliers that stretch the key
+// range), nothing has been moved yet and the function returns nullptr for the caller's other sort. Counts in sh.hist;
+// bin starts and cursors in sortbuf[2048, 4096) (as uint32); pairs placed by bin in sortbuf[1024, 2048), sorted into
+// sortbuf[0, k).
+constexpr uint32_t kBinSortMax = 48;
+__device__ __forceinline__ const uint64_t* bin_sort_desc_1024(SelectShared& sh, int k) {
+    static_assert(kHistBins == 2 * kSelThreads, "two bins per thread");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t* const buf = sh.sortbuf;
+    uint32_t* const cnt = sh.hist;
+    uint32_t* const start = reinterpret_cast<uint32_t*>(buf + 2048);
+    uint32_t* const cur = start + kHistBins;
+    uint64_t* const tmp = buf + 1024;
+    const bool valid = tid < k;
+    const uint64_t x = valid ? buf[tid] : 0ull;
+    const uint32_t key = (uint32_t)(x >> 32);
+    uint32_t mn = valid ? key : 0xffffffffu, mx = valid ? key : 0u;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        mn = min(mn, (uint32_t)__shfl_xor((int)mn, m, 64));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, m, 64));
+    }
+    if (lane == 0) {
+        sh.wave_tot[wave][0] = mn;
+        sh.wave_tot[wave][1] = mx;
+    }
+    cnt[tid] = 0u;
+    cnt[tid + kSelThreads] = 0u;
+    __syncthreads();
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+        kmin = min(kmin, sh.wave_tot[w][0]);
+        kmax = max(kmax, sh.wave_tot[w][1]);
+    }
+    const uint32_t span = kmax - kmin;   // k >= 1, so kmin <= kmax
+    const int shift = span >> 11 ? 32 - __clz((int)span) - 11 : 0;
+    const uint32_t bin = (kmax - key) >> shift;   // < 2048
+    if (valid) atomicAdd(&cnt[bin], 1u);
+    __syncthreads();
+    // exclusive scan of the 2048 counts (thread t: bins 2t, 2t + 1) and the largest count
+    const uint2 c2 = reinterpret_cast<const uint2*>(cnt)[tid];
+    const uint32_t s2 = c2.x + c2.y;
+    const uint32_t inc = wave_incl_scan(s2);
+    uint32_t big = max(c2.x, c2.y);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) big = max(big, (uint32_t)__shfl_xor((int)big, m, 64));
+    __syncthreads();   // every thread has read the minimum and maximum out of wave_tot
+    if (lane == 63) sh.wave_tot[wave][0] = inc;
+    if (lane == 0) sh.wave_tot[wave][1] = big;
+    __syncthreads();
+    uint32_t before = 0u, largest = 0u;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+        before += w < wave ? sh.wave_tot[w][0] : 0u;
+        largest = max(largest, sh.wave_tot[w][1]);
+    }
+    if (largest > kBinSortMax) {
+        __syncthreads();   // the other sort reuses wave_tot
+        return nullptr;
+    }
+    const uint32_t e0 = before + inc - s2;
+    reinterpret_cast<uint2*>(start)[tid] = make_uint2(e0, e0 + c2.x);
+    reinterpret_cast<uint2*>(cur)[tid] = make_uint2(e0, e0 + c2.x);
+    __syncthreads();
+    uint32_t pos = 0u;
+    if (valid) {
+        pos = atomicAdd(&cur[bin], 1u);
+        tmp[pos] = x;
+    }
+    __syncthreads();
+    if (valid) {
+        const uint32_t b0 = start[bin], b1 = cur[bin];
+        uint32_t rank = 0u;
+        for (uint32_t j = b0; j < b1; ++j) {
+            const uint64_t y = tmp[j];
+            rank += (y > x) || (y == x && j < pos);
+        }
+        buf[b0 + rank] = x;
+    }
+    __syncthreads();
+    return buf;
+}
+
 // Score order for 1024 < sort_len(k) <= 4096 staged pairs: the same stable LSD radix sort (passes of 8 bits, each
 // digit complemented so that ascending digit order is descending score; stability keeps equal keys in index order),
 // the pairs taken as up to four sub-blocks of 1024 (sub-block e: pairs 1024 e + t). A pass first counts its digit over
@@ -422,14 +511,19 @@ __device__ __forceinline__ void finish_row(const SelectArgs& a, int row, SelectS
     // descending on (key, ~index): larger score first, then lower index (sortbuf[0, sort_len(k)) was pre-filled by
     // init_sortbuf before the emission)
     __syncthreads();
-    // up to 256 pairs the bitonic sort (a chunk pass of 128 in registers per wave, at most one LDS stride) beats the
-    // radix sort's four barriers per pass; from 512 to 4096 the radix sort wins (k = 128: 2.2 us less per row with
-    // the bitonic sort, k = 1024: 2.7 us less with the radix sort, MI355X); past 4096 the bitonic sort again
-    const uint64_t* sorted = sh.sortbuf;
+    // 128 pairs: the bitonic sort (one chunk pass in registers). 256 to 1024: the bin sort, or where its bins crowd
+    // the bitonic sort (256) or the radix sort (512, 1024). 1025 to 4096: the radix sort by sub-blocks; past 4096 the
+    // bitonic sort. Single-workgroup top-k on MI355X, score order's cost over position order per launch, 32K keys:
+    // k = 1024 3.7 us (radix sort alone 6.0), k = 512 3.3 (radix 4.3), k = 128 2.6 (bitonic; radix 4.0).
+    const uint64_t* sorted = nullptr;
     const int n = sort_len(k);
-    if (n > 256 && n <= kSelThreads) sorted = radix_sort_desc_1024(sh, k);
-    else if (n > kSelThreads && n <= 4 * kSelThreads) sorted = radix_sort_desc_4096(sh, k);
-    else bitonic_sort_desc(sh.sortbuf, n);
+    if (n > 128 && n <= kSelThreads) sorted = bin_sort_desc_1024(sh, k);
+    if (sorted == nullptr) {
+        sorted = sh.sortbuf;
+        if (n > 256 && n <= kSelThreads) sorted = radix_sort_desc_1024(sh, k);
+        else if (n > kSelThreads && n <= 4 * kSelThreads) sorted = radix_sort_desc_4096(sh, k);
+        else bitonic_sort_desc(sh.sortbuf, n);
+    }
     const float* srow = a.scores + (size_t)row * a.score_stride;
     int32_t* ti = a.top_idx ? a.top_idx + (size_t)row * a.top_stride : nullptr;
     float* tv = a.top_val ? a.top_val + (size_t)row * a.top_stride : nullptr;
