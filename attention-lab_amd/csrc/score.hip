@@ -607,7 +607,8 @@ __device__ __forceinline__ float relu_f32(float x) { return __int_as_float(max(_
 //   out[bkg, m] = sum_i w[bkg, i] * act(q[bkg, i, :] . key[bkg, lo + m, :])
 // HBM-bound: 64 key bytes in, 4 score bytes out per position. Lane (quad qd, quarter c) reads dims [8c, 8c + 8) of a
 // key with one 16-byte load, so each load instruction covers 16 whole keys = 1 KiB contiguous; a wave takes 64 keys
-// per group (four loads per lane), double-buffered, and the four waves of a workgroup read adjacent 4 KiB chunks.
+// per group (four loads per lane), three groups in flight, and the four waves of a workgroup read adjacent 4 KiB
+// chunks.
 // With fp16 keys the fp32 query is held as fp16 head + remainder pairs (q = hi + lo) and multiplied with v_dot2_f32_f16
 // (fp32 accumulate); with bf16 keys the keys are widened to fp32. Either way scores keep fp32 accuracy. The quad's partial sums of its 4 keys are reduced and transposed with two
 // DPP steps (xor 1, xor 2), after which lane c holds all heads of key c; ReLU and the head weights follow, and the
@@ -710,16 +711,26 @@ __global__ __launch_bounds__(256) void score_lightning(LightningArgs a) {
     };
     auto run = [&](auto masked_tag) {
         constexpr bool kMasked = decltype(masked_tag)::value;
-        u32x4_t A[4], B[4];
+        // three groups in flight; the host picks 1, 2, 5 or 8 groups per tile, for which no load below reaches past
+        // the tile's last group (such a load would read keys of the next tile: 1/9 more traffic at 8 groups)
+        u32x4_t A[4], B[4], C[4];
         load(0, A);
+        if (a.ng == 1) {
+            process(0, A, kMasked);
+            return;
+        }
+        load(1, B);
         int g = 0;
-        for (; g + 2 <= a.ng; g += 2) {
-            load(g + 1, B);
+        for (; g + 3 <= a.ng; g += 3) {
+            load(g + 2, C);
             process(g, A, kMasked);
-            load(g + 2, A);
+            load(g + 3, A);
             process(g + 1, B, kMasked);
+            load(g + 4, B);
+            process(g + 2, C, kMasked);
         }
         if (g < a.ng) process(g, A, kMasked);
+        if (g + 1 < a.ng) process(g + 1, B, kMasked);
     };
     if (tile_base + 256 * a.ng > a.M) run(std::true_type{});   // the row's last, partial tile
     else run(std::false_type{});
@@ -872,9 +883,10 @@ extern "C" int attnlab_score_lightning(const uint16_t* keys, int key_dtype, cons
     ATTNLAB_REQUIRE(out != nullptr && out_stride >= M, "out must hold M=%d scores per row", M);
     ATTNLAB_REQUIRE(q != nullptr && w != nullptr && reinterpret_cast<uintptr_t>(q) % 16 == 0,
                     "q and w are required; q must be 16-byte aligned");
-    // 64-key groups per wave and tile: tiles of 256..2048 keys, as large as still gives ~1024 workgroups
+    // 64-key groups per wave and tile: tiles of 256..2048 keys, as large as still gives ~1024 workgroups, and one of
+    // 1, 2, 5 or 8 groups (the kernel's three-group pipeline then loads nothing past a tile)
     const int64_t per = (int64_t)M * B * KG / 262144;
-    const int ng = (int)std::min<int64_t>(8, std::max<int64_t>(1, per));
+    const int ng = per >= 8 ? 8 : per >= 5 ? 5 : per >= 2 ? 2 : 1;
     const int tiles = (M + 256 * ng - 1) / (256 * ng);
     LightningArgs a{keys, q, w, out, out_stride, Lk, nh, lo, M, tiles, ng};
     const dim3 grid(B * KG * tiles);
