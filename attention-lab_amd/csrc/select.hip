@@ -566,22 +566,23 @@ struct Emitter {
         if (flat) flat[slot] = base + lo + idx;
     }
 
-    // The set bits of `word`, ascending, as indices idx0 + bit at slots slot, slot + 1, ...: the scores of up to eight
-    // of them are loaded before any is used, so a word costs one memory round trip per eight keys, not one per key.
+    // The set bits of `word`, ascending, as indices idx0 + bit at slots slot, slot + 1, ...: the scores of up to four
+    // of them are loaded before any is used, so a word costs one memory round trip per four keys, not one per key
+    // (eight at a time pushed select_resolve to 120 VGPRs and 152 bytes of scratch per lane).
     __device__ __forceinline__ void put_word(uint32_t word, int idx0, uint32_t& slot) const {
         const bool need = order == ATTNLAB_ORDER_SCORE || tv != nullptr;
         while (word) {
-            int ix[8];
-            float v[8];
+            int ix[4];
+            float v[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 4; ++u) {
                 ix[u] = word ? idx0 + (int)(__ffs(word) - 1) : -1;
                 word &= word - 1u;   // stays 0 once empty
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = (need && ix[u] >= 0) ? srow[ix[u]] : 0.0f;
+            for (int u = 0; u < 4; ++u) v[u] = (need && ix[u] >= 0) ? srow[ix[u]] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < 4; ++u)
                 if (ix[u] >= 0) put(slot++, ix[u], v[u]);
         }
     }
@@ -1209,9 +1210,10 @@ __global__ __launch_bounds__(kSelThreads) void select_resolve(SelectArgs a, Tile
         for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
         return;
     }
+    // the words again from the LDS bitmap (a loop that needs no unrolled register copy)
     const Emitter em = make_emitter(a, row, sh);
-#pragma unroll
-    for (int j = 0; j < kMaxWordsPerThread; ++j) em.put_word(sw[j], (w0 + j) * 32, slot);
+    for (int j = 0; j < wpt; ++j)
+        if (w0 + j < W) em.put_word(bits[w0 + j], (w0 + j) * 32, slot);
     for (int i = tid; i < kSelectStateWords; i += kSelThreads) st[i] = 0u;
     __syncthreads();
     finish_row(a, row, sh);   // F positions; in score order the sort and the outputs
