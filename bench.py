@@ -104,6 +104,10 @@ def parse_args():
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
+    ap.add_argument("--index-build-workload", action="store_true",
+                    help="instead of the bench line: the bulk index-table build (project_keys, bf16 and float32) "
+                         "at B=16, G=8, T=32768, d=128, r=32, 10 HIP-event-timed launches each; one JSON line (also "
+                         "the command profiled for these kernels)")
     ap.add_argument("--prefill-pmc-summary", metavar="DIR",
                     help="summarise a rocprofv3 --pmc pass of --prefill-workload (SQ_VALU_MFMA_BUSY_CYCLES, "
                          "GRBM_GUI_ACTIVE, SQ_INSTS_MFMA, SQ_INSTS_VALU) into the matrix-core busy fraction")
@@ -506,6 +510,42 @@ def prefill_workload(torch, dev):
     torch.cuda.synchronize()
     print(json.dumps({"prefill_workload": f"{PREFILL_KERNEL} x5", "scores": ps.scores(),
                       "algorithmic_bytes": ps.algorithmic_bytes(), "flops": ps.flops()}))
+    return 0
+
+
+def index_build_workload(torch, dev, reps=10, B=16, G=8, T=32768, d=128, r=32):
+    """The prefill's bulk index-table build, zT[b, g, :, t] = wk[g] . k_pre[b, g, t] for a whole 32K context
+    (qwen_wrap.py:320-324 builds it per layer from the prompt's pre-RoPE keys), in bf16 (project_keys_mfma) and in
+    float32 (project_keys_f32_mfma, a trained bank's dtype). Algorithmic bytes per position: d keys read and r table
+    entries written."""
+    from attention_lab import _native as nat
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {"index_build_workload": f"B={B}, G={G}, T={T}, d={d}, r={r}", "launches": reps}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    for name, dtype, fn in (("bf16", torch.bfloat16, "attnlab_project_keys"),
+                            ("f32", torch.float32, "attnlab_project_keys_f32")):
+        k_pre = torch.randn(B, G, T, d, device=dev, generator=gen).to(dtype)
+        wk = (torch.randn(G, r, d, device=dev, generator=gen) * 0.05).to(dtype)
+        zT = torch.empty(B, G, r, T, device=dev, dtype=dtype)
+
+        def launch():
+            nat.call(fn, k_pre.data_ptr(), T * d, d, wk.data_ptr(), zT.data_ptr(), B, G, T, r, d, T, 0, stream)
+        launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()   # torch's current stream, the stream the kernels launch on
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = B * G * T * (d + r) * k_pre.element_size()
+        out[name] = {"avg_launch_us": us, "algorithmic_bytes": nbytes, "gbs": nbytes / us / 1e3,
+                     "hbm_frac": nbytes / us / 1e3 / PEAK_HBM_GBS}
+        del k_pre, wk, zT
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
     return 0
 
 
@@ -1351,6 +1391,8 @@ def main() -> int:
         return pmc_workload(torch, dev, args)
     if args.prefill_workload:
         return prefill_workload(torch, dev)
+    if args.index_build_workload:
+        return index_build_workload(torch, dev)
     if args.sweeps:
         return run_sweeps(torch, dev, args.sweeps)
     if args.c4:
