@@ -318,6 +318,7 @@ struct ProjectF32Args {
     const float* wk;
     float* zT;
     int G, T, r, d, C, col0, tiles;
+    int vec4 = 0;   // zT columns col0 + 4i are 16-byte aligned (16-byte stores)
 };
 
 __global__ __launch_bounds__(256) void project_keys_f32(ProjectF32Args a) {
@@ -363,9 +364,13 @@ __global__ __launch_bounds__(256) void project_keys_f32(ProjectF32Args a) {
 constexpr int kPkmPos = 256;
 constexpr int kPkmPitch = 128 + 4;   // floats per staged weight row
 
+constexpr int kZPitch = 68;   // floats per staged output row (64 positions + 4)
+
 template <int MT, int PC>   // PC: d / 16 fixed at compile time (every key load issued before the first product), or 0
 __global__ __launch_bounds__(256) void project_keys_f32_mfma(ProjectF32Args a) {
-    __shared__ __attribute__((aligned(16))) float ws[16 * MT * kPkmPitch];
+    // the weight rows, then the four waves' staged output tiles
+    constexpr int kWsFloats = 16 * MT * kPkmPitch > 4 * 16 * kZPitch ? 16 * MT * kPkmPitch : 4 * 16 * kZPitch;
+    __shared__ __attribute__((aligned(16))) float ws[kWsFloats];
     const int bg = blockIdx.x / a.tiles, tile = blockIdx.x - bg * a.tiles;
     const int g = bg % a.G;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -436,17 +441,38 @@ __global__ __launch_bounds__(256) void project_keys_f32_mfma(ProjectF32Args a) {
             }
         }
     }
+    // Output through LDS (the weight rows are no longer read once every wave is past the products): a wave stages
+    // each 16-row tile as 16 x 64 floats, then writes every row's 64 positions as 256 contiguous bytes (16 lanes x
+    // 16 bytes) instead of 64-byte runs. Row pitch 68 floats: the staging stores of lane groups q and q + 1 fall in
+    // different banks.
+    __syncthreads();
+    float* zs = ws + wave * 16 * kZPitch;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            const int t = t0 + 16 * nt + c;
+        for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = 16 * mt + 4 * q + i;
-                if (j < a.r && t < a.T) a.zT[((size_t)bg * a.r + j) * a.C + a.col0 + t] = acc[mt][nt][i];
+            for (int i = 0; i < 4; ++i) zs[(4 * q + i) * kZPitch + 16 * nt + c] = acc[mt][nt][i];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int row = 4 * it + (lane >> 4);
+            const int j = 16 * mt + row;
+            const int tp = t0 + 4 * (lane & 15);
+            const float4 v = *reinterpret_cast<const float4*>(&zs[row * kZPitch + 4 * (lane & 15)]);
+            if (j < a.r) {
+                float* dst = a.zT + ((size_t)bg * a.r + j) * a.C + a.col0 + tp;
+                if (a.vec4 && tp + 3 < a.T) {
+                    *reinterpret_cast<float4*>(dst) = v;
+                } else {
+                    if (tp < a.T) dst[0] = v.x;
+                    if (tp + 1 < a.T) dst[1] = v.y;
+                    if (tp + 2 < a.T) dst[2] = v.z;
+                    if (tp + 3 < a.T) dst[3] = v.w;
+                }
             }
         }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -546,6 +572,7 @@ extern "C" int attnlab_project_keys_f32(const float* k_pre, int64_t k_bg_stride,
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (d % 16 == 0) {
         ProjectF32Args a{k_pre, k_bg_stride, k_row_stride, wk, zT, G, T, r, d, C, col0, (T + kPkmPos - 1) / kPkmPos};
+        a.vec4 = C % 4 == 0 && col0 % 4 == 0 && reinterpret_cast<uintptr_t>(zT) % 16 == 0;
         const dim3 grid(B * G * a.tiles), block(256);
         if (r <= 16) {
             if (d == 128) hipLaunchKernelGGL((project_keys_f32_mfma<1, 8>), grid, block, 0, s, a);

@@ -103,6 +103,26 @@ def test_project_queries_and_keys(gpu):
     check_sum(one, want, terms, "bulk build")
 
 
+@pytest.mark.parametrize("d,r,C", [(128, 16, 704), (128, 20, 702), (64, 32, 702), (96, 8, 705), (40, 32, 704)])
+def test_project_keys_shapes(gpu, d, r, C):
+    """Matrix-core build (d a multiple of 16: one or two 16-row tiles, the compile-time loop at d = 128, the runtime
+    loop elsewhere) and the scalar build (d = 40): columns that are not 4-aligned (4-byte stores after the staged
+    tile), chunk ends inside a 256-position workgroup, every column within the sum bound of the exact value."""
+    B, G, T = 2, 3, 700
+    gen = torch.Generator().manual_seed(d + r)
+    k_pre = torch.randn(B, G, C, d, generator=gen).to(gpu)
+    wk = (0.02 * torch.randn(G, r, d, generator=gen)).to(gpu)
+    table = torch.full((B, G, r, C), float("nan"), device=gpu)
+    bounds = [0, 5, 333, T]
+    for a, b in zip(bounds, bounds[1:]):
+        project_keys(k_pre[:, :, a:b], wk, out=table, col0=a)
+    torch.cuda.synchronize()
+    want = exact.project_keys(a64(k_pre[:, :, :T]), a64(wk))
+    terms = exact.project_keys(np.abs(a64(k_pre[:, :, :T])), np.abs(a64(wk)))
+    check_sum(table[..., :T], want, terms, f"bulk build d={d} r={r}")
+    assert bool(torch.isnan(table[..., T:]).all()), "columns past the last chunk were written"
+
+
 def test_project_keys_validation(gpu):
     idx = GroupedIndexer(2, 2, 128, 32, device=gpu, dtype=torch.float32, seed=1)
     k = torch.randn(1, 2, 10, 128, device=gpu)
