@@ -142,3 +142,18 @@ def test_topk_picks_the_tiled_kernels_by_row_length_and_count():
     assert not hip_select.use_tiled(128, 32768) and not hip_select.use_tiled(256, 32768)
     assert hip_select.use_tiled(256, 65536) and hip_select.use_tiled(512, 262144)
     assert not hip_select.use_tiled(1, 262145)
+
+
+def test_build_refuses_kernels_with_scratch_memory():
+    """build() compiles with the compiler's resource report and fails on any kernel that uses scratch memory (a
+    register array or spill placed in memory); the parser reads the report's kernel name and scratch size."""
+    import __graft_entry__ as ge
+    remarks = "\n".join([
+        "x.hip:1:1: remark: Function Name: _ZN7attnlab4goodEv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs: 53 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark: Function Name: _ZN7attnlab3badEv [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 152 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert ge.scratch_kernels(remarks) == [("_ZN7attnlab3badEv", 152)]
+    assert ge.scratch_kernels("") == []
