@@ -190,6 +190,24 @@ def test_lightning_matches_oracle(gpu, dtype, nh, relu):
     assert np.abs(f64(s) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("B,KG,L,ngroups", [(1, 8, 70000, 2), (2, 8, 90000, 5), (2, 8, 140000, 8)])
+def test_lightning_long_rows_every_pipeline_depth(gpu, B, KG, L, ngroups):
+    """Rows long enough for 2, 5 and 8 64-key groups per wave and tile (the kernel's three-group pipeline, whose group
+    counts leave no load past a tile), the last tile of each row partial, lo > 0; against the float64 oracle."""
+    nh = 4
+    gen = torch.Generator().manual_seed(L)
+    keys = (torch.randn(B, KG, L, 32, generator=gen) / 32 ** 0.5).to(torch.float16)
+    q = torch.randn(B, KG, nh, 32, generator=gen)
+    w = torch.rand(B, KG, nh, generator=gen)
+    lo, hi = 68, L - 3
+    per = (hi - lo) * B * KG // 262144   # the host's groups per tile: 8, 5, 2 or 1, the largest not above per
+    assert (8 if per >= 8 else 5 if per >= 5 else 2 if per >= 2 else 1) == ngroups
+    s = hip_score.score_lightning(keys.to(gpu), q.to(gpu), w.to(gpu), lo, hi, relu=True)
+    torch.cuda.synchronize()
+    ref = exact.lightning_scores(f64(keys), f64(q), f64(w), lo, hi, True)
+    assert np.abs(f64(s) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
 def test_lightning_reduces_to_grouped_mode(gpu):
     """nh = 1, w = 1, identity activation, keys = zT transposed: the lightning kernel must equal the grouped scan."""
     B, G, C = 2, 8, 3000
