@@ -155,14 +155,15 @@ int score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, 
 struct FusedGeometry {
     int nsub, tiles;
 };
-// Sub-tiles per workgroup: 8, 4 or 2, as many as still leave 1024 workgroups (each workgroup's tail, the histogram
-// flush and the key list, then runs as rarely as the chip's occupancy allows); small grids (B = 1 at 32K) take 2 while
-// 256 workgroups remain (one per CU: half as many lists for the select to read, the latency of one workgroup's chain
-// unchanged); else 1.
+// Sub-tiles per workgroup: 8, 4 or 2, as many as still leave 256 workgroups (one per CU), else 1. Fewer, longer
+// workgroups run each one's tail (the histogram flush and the key list) less often and leave the select fewer lists
+// to read: at 32K, per layer, B=2 26.1 against 27.0 us for the earlier rule (as many as leave 1024 workgroups, 2 for
+// small grids), B=4 34.1 against 36.5, B=8 49.6 against 50.9; float32 tables B=4 46.3 against 52.5. B=1 (2 sub-tiles,
+// 256 workgroups) and B=16 (8 sub-tiles, 1024 workgroups) tile as before.
 inline FusedGeometry fused_tiling(int BG, int lo, int hi) {
     const int span = ((hi + 7) & ~7) - (lo & ~7);
     const int64_t blocks512 = (int64_t)BG * ((span + 511) / 512);
-    const int nsub = blocks512 >= 8 * 1024 ? 8 : blocks512 >= 4 * 1024 ? 4 : blocks512 >= 2 * 256 ? 2 : 1;
+    const int nsub = blocks512 >= 8 * 256 ? 8 : blocks512 >= 4 * 256 ? 4 : blocks512 >= 2 * 256 ? 2 : 1;
     return FusedGeometry{nsub, (span + 512 * nsub - 1) / (512 * nsub)};
 }
 FusedGeometry fused_geometry(int BG, int C, int r, int hd, int lo, int hi, const void* zT, bool u_given);

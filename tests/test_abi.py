@@ -87,7 +87,7 @@ def test_select_scratch_formula(native_lib):
 
 def list_region(BG, lo, hi, k):
     """The score kernel's per-workgroup key lists: workgroups of 8, 4 or 2 sub-tiles of 512 columns (as many as leave
-    1024 workgroups), 2 for small grids while 256 workgroups remain, else 1, a list of at least lmin = s + 3 floor(sqrt(s)) + 16 keys for the even share
+    256 workgroups), else 1, a list of at least lmin = s + 3 floor(sqrt(s)) + 16 keys for the even share
     s = ceil(k * n / M) of n keys per workgroup and at most cap = min(n, lmin + 192 rounded up to 64) entries of 8
     bytes, and an 8-byte header per workgroup. None where the list select does not apply (M > 32768, more than 128
     workgroups per row, 2 * lmin > n)."""
@@ -96,7 +96,7 @@ def list_region(BG, lo, hi, k):
         return 0
     span = ((hi + 7) & ~7) - (lo & ~7)
     blocks = BG * ((span + 511) // 512)
-    nsub = 8 if blocks >= 8 * 1024 else 4 if blocks >= 4 * 1024 else 2 if blocks >= 2 * 256 else 1
+    nsub = 8 if blocks >= 8 * 256 else 4 if blocks >= 4 * 256 else 2 if blocks >= 2 * 256 else 1
     n = 512 * nsub
     tiles = (span + n - 1) // n
     share = (k * n + M - 1) // M
