@@ -1375,8 +1375,8 @@ def main() -> int:
     if args.prefill_pmc_summary:
         return prefill_pmc_summary(args.prefill_pmc_summary)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one GPU, and the "
-                                   "multi-GPU design (tensor parallel by KV group) is described in DESIGN.md, not run",
+        print(json.dumps({"error": "this build runs on one GPU only: every GPU box here has one GPU; splitting "
+                                   "the step over GPUs (tensor parallel by KV group) is designed, not built or run",
                           "n_gpus": args.gpus}))
         return 2
     import torch
