@@ -185,9 +185,10 @@ def sparse_partitions(BG: int, rows: int, h: int = 1) -> int:
     dividing h) until the grid reaches one workgroup per CU; those count towards the 256 workgroups. With four head
     groups and at least 32 (b, g) rows the target is 512: splitting the rows further beats splitting the heads there
     (MI355X, 32K, S = 1092, per layer: B=4, h=4 33.2 us at P=4 against 34.1 at P=2; B=8 48.8 at P=2 against 49.5 at
-    P=1; with eight head groups, B=4, the 256 target is 0.2 us better)."""
+    P=1; with eight head groups, B=4, the 256 target is 0.2 us better). With one head per KV group and at least 128
+    (b, g) rows it is 128 (B=16, h=1: 73.7 us at P=1 against 74.3 at P=2; B=8 keeps P=4, 45.6 us)."""
     hg = h & -h if h > 0 else 1   # largest power of two dividing h
-    blocks = 512 if hg == 4 and BG >= 32 else 256
+    blocks = 512 if hg == 4 and BG >= 32 else 128 if hg == 1 and BG >= 128 else 256
     return auto_partitions(BG * hg, rows, max_p=MAX_P, min_rows=128, blocks=blocks)
 
 
