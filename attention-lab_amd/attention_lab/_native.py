@@ -15,7 +15,7 @@ import torch
 
 LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
 SELECT_STATE_WORDS = 2112
@@ -43,8 +43,8 @@ SIGNATURES = {
     "attnlab_topk_tiled": (_i, [_p, _i64] + [_i] * 4 + [_p, _p, _i64, _p, _p, _i64, _p]),
     "attnlab_select_rows": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
     "attnlab_select_scratch_bytes": (_i64, [_i] * 4),
-    "attnlab_list_bytes": (_i64, [_i] * 5),
-    "attnlab_score_grouped_lists": (_i, [_p] * 7 + [_i64] + [_i] * 10 + [_p, _p, _i64, _p]),
+    "attnlab_list_bytes": (_i64, [_i] * 6),
+    "attnlab_score_grouped_lists": (_i, [_p] * 7 + [_i64] + [_i] * 11 + [_p, _p, _i64, _p]),
     "attnlab_select_lists": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
@@ -125,17 +125,40 @@ class Workspace:
     state).
 
     Buffers are zero-filled when allocated: the select state (top-k histograms and counters) must start at zero, and
-    the kernels leave it zeroed after every call. Two launches that share one Workspace must be ordered on one stream. Grow it (one eager
-    call) before capturing the launches in a HIP graph, so no allocation happens under capture.
+    the kernels leave it zeroed after every call. Two launches that share one Workspace must be ordered on one stream.
+
+    HIP graphs: a captured launch keeps the address of the buffer it was given. A buffer that a larger call replaces is
+    therefore never freed here: it is retired but kept alive, so a graph captured before the growth still replays into
+    memory nobody else owns (and its select state, left zeroed by every call, stays valid). Growth takes slack
+    (a quarter more, at least 1 MiB) so that a decode loop whose sizes creep up step by step reallocates rarely.
+    Growing while the current stream is capturing raises RuntimeError: grow it with one eager call of the largest
+    shape first. `release_retired()` frees the retired buffers once no graph that used them will replay.
     """
+
+    SLACK_MIN = 1 << 20
 
     def __init__(self):
         self._bytes: dict = {}
+        self._retired: list = []
 
     def bytes(self, device: torch.device, nbytes: int, tag: str = "main") -> torch.Tensor:
         key = (device, tag)
         buf = self._bytes.get(key)
+        nbytes = max(int(nbytes), 256)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(f"workspace '{tag}' must grow to {nbytes} bytes during HIP graph capture; run one "
+                                   "eager call of this shape before capturing")
+            if buf is not None:
+                self._retired.append(buf)   # a captured graph may still hold its address
+                nbytes = max(nbytes, buf.numel() + max(buf.numel() // 4, self.SLACK_MIN))
+            buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
             self._bytes[key] = buf
         return buf
+
+    def retired_bytes(self) -> int:
+        return sum(int(b.numel()) for b in self._retired)
+
+    def release_retired(self) -> None:
+        """Free the buffers replaced by growth (only when no captured graph that used them replays again)."""
+        self._retired.clear()

@@ -208,17 +208,19 @@ def gathered_decode_step_kernel(q_main, k_cache, v_cache, rows, selected_count: 
     return out.view(B, G, h, 1, d)
 
 
-_STEP_WS = nat.Workspace()   # scores / row list / partials of sparse_decode_step_kernel, grown on demand
+_STEP_WS = nat.Workspace()   # scores / row list / partials and the select state of sparse_decode_step_kernel
 
 
 def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, wk, fixed_rows, off_lo, lo: int,
                               hi: int, k: int, selected_count: int, *, k_pre_new=None, write_col: int = -1,
                               scale=None, backend="sdpa", return_rows: bool = False, canonical_order: bool = False,
-                              partitions=None):
+                              partitions=None, workspace=None):
     """One layer's D read for one new query (T == 1) as three HIP launches; same contract as decode.py:145-163.
 
     `return_rows=True` also returns the flat row ids that were read. canonical_order=True lists every row set in
-    ascending position; otherwise F comes first and the candidates follow by descending score.
+    ascending position; otherwise F comes first and the candidates follow by descending score. `workspace` (a
+    _native.Workspace; default: one shared by the module) holds the step's scratch and select state; see Workspace
+    for HIP graph capture.
     """
     if backend not in SUBSET_BACKENDS:
         raise ValueError(f"unknown subset backend {backend!r}")
@@ -271,9 +273,10 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     sc = float(1.0 / math.sqrt(d) if scale is None else scale)
     order = nat.ORDER_POSITION if canonical_order else nat.ORDER_SCORE
     nbytes = nat.lib().attnlab_sparse_decode_workspace(B, G, h, lo, hi, legal, k, P)
-    ws = _STEP_WS.bytes(k_cache.device, nbytes, "step")
+    wsp = _STEP_WS if workspace is None else workspace
+    ws = wsp.bytes(k_cache.device, nbytes, "step")
     # select state: zeroed once, left zeroed by each call
-    state = _STEP_WS.bytes(k_cache.device, B * G * nat.SELECT_STATE_WORDS * 4, "state")
+    state = wsp.bytes(k_cache.device, B * G * nat.SELECT_STATE_WORDS * 4, "state")
     out = torch.empty(B, G, h, d, dtype=torch.bfloat16, device=k_cache.device)
     flat = torch.empty(B * G * S, dtype=torch.int64, device=k_cache.device) if return_rows else None
     entry = "attnlab_sparse_decode_step" if idx_dt == torch.bfloat16 else "attnlab_sparse_decode_step_f32"

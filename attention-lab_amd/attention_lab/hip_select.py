@@ -5,9 +5,10 @@ lower candidate index, NaN ranks below every number, -0.0 equals +0.0. `topk` re
 torch.topk(..., sorted=True) on the last dimension, for any k in either order; `select_rows` writes the whole row list
 of a decode step (F merged with the chosen candidates) in the layout the attend kernel reads.
 
-The tiled kernels' select state and scratch live in a module workspace that grows on demand and is never freed, so
-after one eager call of a shape the same calls allocate nothing and can be captured in a HIP graph. Calls that share it
-must be ordered on one stream (torch's current stream, where every call launches).
+The tiled kernels' select state and scratch live in a module workspace (or one the caller passes as `workspace=`) that
+grows on demand and keeps every buffer it ever handed out alive, so after one eager call of a shape the same calls
+allocate nothing and can be captured in a HIP graph, and a later growth never frees memory a captured graph still
+uses. Calls that share it must be ordered on one stream (torch's current stream, where every call launches).
 """
 from __future__ import annotations
 
@@ -38,7 +39,7 @@ def use_tiled(R: int, M: int) -> bool:
     return TILED_MIN_M <= M <= TILED_MAX_M and not (M <= REG_MAX_M and R >= REG_MIN_ROWS)
 
 
-def topk(scores, k: int, *, order: str = "score", tiled=None):
+def topk(scores, k: int, *, order: str = "score", tiled=None, workspace=None):
     """Top-k over the last dim of fp32 `scores` [..., M] -> (values fp32 [..., k], indices int64 [..., k]).
 
     order="score": descending score, ties lowest index first (torch.topk's sorted order with ties defined);
@@ -66,10 +67,11 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
         tiled = use_tiled(R, M)
     if code == nat.ORDER_SCORE and k > LDS_SORT_K:
         tiled = True   # the radix pass of a long score order runs in the tiled entry's scratch
+    ws = _WS if workspace is None else workspace
     if R and k and tiled:
-        state = _WS.bytes(scores.device, R * nat.SELECT_STATE_WORDS * 4, "state")
+        state = ws.bytes(scores.device, R * nat.SELECT_STATE_WORDS * 4, "state")
         nbytes = nat.lib().attnlab_select_scratch_bytes(R, M, k, code)
-        scratch = _WS.bytes(scores.device, nbytes, "scratch")
+        scratch = ws.bytes(scores.device, nbytes, "scratch")
         nat.call("attnlab_topk_tiled", s2.data_ptr(), s2.stride(0), R, M, k, code, idx.data_ptr(), val.data_ptr(),
                  idx.stride(0), state.data_ptr(), scratch.data_ptr(), scratch.numel(), nat.stream_of(scores.device))
     elif R and k:
@@ -79,7 +81,7 @@ def topk(scores, k: int, *, order: str = "score", tiled=None):
 
 
 def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, order: str = "position",
-                rows=None, want_flat: bool = False, state=None, tiled: bool = True):
+                rows=None, want_flat: bool = False, state=None, tiled: bool = True, workspace=None):
     """Row list of one decode step from candidate scores [B, G, hi-lo] (fp32, unit column stride).
 
     Returns (rows int32 [B, G, S] original positions, flat int64 [B*G*S] row ids of the flattened cache or None),
@@ -117,7 +119,7 @@ def select_rows(scores, lo: int, hi: int, legal: int, k: int, capacity: int, *, 
     scratch = None
     if k > 0 and ((state is not None and tiled) or (code == nat.ORDER_SCORE and k > LDS_SORT_K)):
         nbytes = nat.lib().attnlab_select_scratch_bytes(B * G, M, k, code)
-        scratch = _WS.bytes(scores.device, nbytes, "scratch")
+        scratch = (_WS if workspace is None else workspace).bytes(scores.device, nbytes, "scratch")
     nat.call("attnlab_select_rows", scores.data_ptr(), stride, B, G, lo, hi, legal, k, capacity, code,
              rows.data_ptr(), S, nat.ptr(flat), nat.ptr(state), nat.ptr(scratch),
              0 if scratch is None else scratch.numel(), nat.stream_of(scores.device))

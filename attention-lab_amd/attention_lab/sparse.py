@@ -59,8 +59,14 @@ def subset_attention(q, k_sub, v_sub, valid_mask=None, *, scale=None, backend="s
     """Attention of q [B,G,h,T,d] over a gathered subset k_sub, v_sub [B,G,S,d] -> [B,G,h,T,d] (sparse.py:40-60).
 
     The h*T query rows of a group share the S subset rows (each row is read once per group), so the T queries fold
-    into the head axis of the attend kernel: h*T <= 8 rows per group, bfloat16, d = 128. valid_mask [B,G,S] (bool)
-    drops padded slots; a group with no valid slot has no defined output.
+    into the head axis of the attend kernel. valid_mask [B,G,S] (bool) drops padded slots; a group with no valid slot
+    has no defined output.
+
+    Narrower than the reference, which takes any dtype and head dim through torch: this runs only on the HIP attend
+    kernel, so q, k_sub and v_sub must be bfloat16 on a HIP device with d = 128 and h*T <= 8 query rows per group;
+    other inputs raise ValueError naming the restriction (there is no torch fallback). Both backend names run that
+    one kernel: "sdpa" and "explicit" compute the same softmax attention and differ only in rounding in the
+    reference, and the kernel accumulates in fp32 either way.
     """
     if backend not in ("sdpa", "explicit"):
         raise ValueError(f"unknown subset backend {backend!r}")
@@ -70,8 +76,14 @@ def subset_attention(q, k_sub, v_sub, valid_mask=None, *, scale=None, backend="s
     S = int(k_sub.shape[2])
     if tuple(k_sub.shape[:2]) != (B, G) or k_sub.shape[3] != d:
         raise ValueError(f"subset {tuple(k_sub.shape)} does not match q {tuple(q.shape)}")
+    for t, n in ((q, "q"), (k_sub, "k_sub"), (v_sub, "v_sub")):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"subset_attention on the HIP attend kernel takes bfloat16 only; {n} is {t.dtype}")
+    if d != hip_attend.HEAD_DIM:
+        raise ValueError(f"subset_attention on the HIP attend kernel takes head_dim {hip_attend.HEAD_DIM} only, got {d}")
     if h * T > hip_attend.MAX_H:
-        raise ValueError(f"h*T = {h * T} query rows per group exceed the kernel's {hip_attend.MAX_H}")
+        raise ValueError(f"subset_attention on the HIP attend kernel takes h*T <= {hip_attend.MAX_H} query rows per "
+                         f"group, got {h * T}")
     slots = torch.arange(S, device=k_sub.device, dtype=torch.int32).expand(B, G, S)
     if valid_mask is not None:
         if tuple(valid_mask.shape) != (B, G, S):

@@ -85,8 +85,10 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     float* part = P > 1 ? reinterpret_cast<float*>(ws + L.part) : nullptr;
     const int S = lo + (legal - hi) + k;
     const int d = 128;
-    // the list select (it needs the select state): lists in the select scratch region
-    const ListPlan plan = k > 0 && state ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
+    // the list select (it needs the select state, and sorts at most kMaxScoreOrderK picks by score): lists in the
+    // select scratch region; otherwise the tiled select, whose scratch (sized for score order) holds the radix sort's
+    // buffers
+    const ListPlan plan = k > 0 && state && !staged_score_order(order, k) ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
     const ScoreLists lists = plan.cap > 0 ? list_layout(ws + L.sel, B * G, geo, plan) : ScoreLists{};
     int rc;
     if (k > 0) {

@@ -833,18 +833,23 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
     return check_launch("score_scan");
 }
 
-extern "C" int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k) {
+extern "C" int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k, int order) {
     if (B < 1 || G < 1 || lo < 0 || hi < lo || k < 0 || k > hi - lo) return -1;
-    return list_region_bytes((int64_t)B * G, lo, hi, k);
+    if (order != ATTNLAB_ORDER_POSITION && order != ATTNLAB_ORDER_SCORE) return -1;
+    return staged_score_order(order, k) ? 0 : list_region_bytes((int64_t)B * G, lo, hi, k);
 }
 
 extern "C" int attnlab_score_grouped_lists(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk,
                                            const uint16_t* q_cat, const uint16_t* wq_t, float* u_out, float* out,
                                            int64_t out_stride, int B, int G, int r, int C, int d, int hd, int lo,
-                                           int hi, int write_col, int k, uint32_t* state, void* lists,
+                                           int hi, int write_col, int k, int order, uint32_t* state, void* lists,
                                            int64_t lists_bytes, void* stream) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && 0 <= lo && lo <= hi && 0 <= k && k <= hi - lo,
                     "need B, G >= 1, 0 <= lo <= hi and 0 <= k <= hi - lo (B=%d G=%d lo=%d hi=%d k=%d)", B, G, lo, hi, k);
+    ATTNLAB_REQUIRE(order == ATTNLAB_ORDER_POSITION || order == ATTNLAB_ORDER_SCORE, "unknown order %d", order);
+    // refused here, before the state is touched: the list select sorts at most kMaxScoreOrderK picks by score
+    ATTNLAB_REQUIRE(!staged_score_order(order, k), "the list select sorts at most %d rows in score order (k=%d); "
+                    "attnlab_score_grouped with attnlab_select_rows takes larger k", kMaxScoreOrderK, k);
     const FusedGeometry geo = fused_geometry(B * G, C, r, hd, lo, hi, zT, false);
     const ListPlan plan = list_plan(hi - lo, k, geo);
     ATTNLAB_REQUIRE(plan.cap > 0, "the list select does not apply: it needs the one-launch score (r = 32, h*d <= 512, "

@@ -18,6 +18,13 @@ constexpr int kSuperBins = kHistBins / 32;
 constexpr int kSelectStateWords = kHistBins + kSuperBins;
 static_assert(kSelectStateWords == 2112, "ABI: ATTNLAB_SELECT_STATE_WORDS");
 
+// Score order sorts up to this many selected pairs in LDS (64 KB); past it the select stages the picks in position
+// order and a radix pass over a scratch buffer lists them by score (only the tiled and single-workgroup selects).
+constexpr int kMaxScoreOrderK = ATTNLAB_LDS_SORT_K;
+__host__ __device__ inline bool staged_score_order(int order, int k) {
+    return order == ATTNLAB_ORDER_SCORE && k > kMaxScoreOrderK;
+}
+
 // Order-preserving key: larger float -> larger key; -0 -> +0; NaN -> 0 (below -inf, whose key is 0x007fffff).
 __device__ __forceinline__ uint32_t score_key(float f) {
     if (f != f) return 0u;

@@ -23,7 +23,6 @@ namespace attnlab {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kMaxScoreOrderK = 8192;   // score order sorts the k selected pairs in LDS (64 KB)
 
 struct SelectArgs {
     const float* scores;
@@ -1513,10 +1512,6 @@ __host__ __device__ inline int64_t sort_scratch_bytes(int R, int k) {
     return align_bytes((int64_t)R * k * 4, 256) + 2 * align_bytes((int64_t)R * k * 8, 256);
 }
 
-__host__ __device__ inline bool staged_score_order(int order, int k) {
-    return order == ATTNLAB_ORDER_SCORE && k > kMaxScoreOrderK;
-}
-
 struct SortShared {
     uint16_t cnt[kSelWaves][kHistBins];   // this tile's count of each digit per wave, zero between tiles
     uint32_t base[kHistBins];             // first slot of each digit in this pass
@@ -1808,6 +1803,8 @@ extern "C" int attnlab_select_lists(const float* scores, int64_t score_stride, i
     const FusedGeometry geo = fused_tiling(B * G, lo, hi);
     const ListPlan plan = hi > lo ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
     ATTNLAB_REQUIRE(plan.cap > 0, "the list select does not apply to B*G=%d, M=%d, k=%d", B * G, hi - lo, k);
+    ATTNLAB_REQUIRE(!staged_score_order(order, k), "the list select sorts at most %d rows in score order (k=%d); "
+                    "attnlab_select_rows takes larger k", kMaxScoreOrderK, k);
     ATTNLAB_REQUIRE(state != nullptr && (reinterpret_cast<uintptr_t>(state) & 15) == 0,
                     "the list select needs the 16-byte aligned select state");
     ATTNLAB_REQUIRE(lists != nullptr && (reinterpret_cast<uintptr_t>(lists) & 255) == 0 &&

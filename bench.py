@@ -306,7 +306,7 @@ def launchers(ls, torch):
     sel_bytes = lib.attnlab_select_scratch_bytes(B * G, ls.M, ls.k, nat.ORDER_POSITION)
     sel_scratch = torch.empty(sel_bytes, dtype=torch.uint8, device=dev)
     # the list select (what the fused step runs where it applies): the score kernel's key lists
-    list_bytes = lib.attnlab_list_bytes(B, G, ls.lo, ls.hi, ls.k)
+    list_bytes = lib.attnlab_list_bytes(B, G, ls.lo, ls.hi, ls.k, nat.ORDER_POSITION)
     lists = torch.empty(max(list_bytes, 256), dtype=torch.uint8, device=dev)
     u_buf = torch.zeros(B * G * r, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(d)
@@ -329,8 +329,8 @@ def launchers(ls, torch):
         if list_bytes > 0:
             nat.call("attnlab_score_grouped_lists", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
                      ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), u_buf.data_ptr(), ls.scores.data_ptr(),
-                     ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, ls.k, hist.data_ptr(),
-                     lists.data_ptr(), list_bytes, stream())
+                     ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, ls.k, nat.ORDER_POSITION,
+                     hist.data_ptr(), lists.data_ptr(), list_bytes, stream())
             return
         nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
                  ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), None, u_buf.data_ptr(), ls.scores.data_ptr(),

@@ -202,13 +202,19 @@ int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G,
  * writes what attnlab_select_rows writes for the same scores, state and arguments, reading the lists instead of every
  * score (a tile whose list cannot hold its part of the selection is read from the scores), in one launch, and leaves
  * the state zeroed. attnlab_list_bytes returns 0 where the list select does not apply (hi - lo > 32768, or k large
- * against hi - lo; both functions then fail with ATTNLAB_EINVAL) and -1 for invalid sizes.
+ * against hi - lo, or `order` ATTNLAB_ORDER_SCORE with k > ATTNLAB_LDS_SORT_K, which the list select does not sort;
+ * both functions then fail with ATTNLAB_EINVAL before any launch) and -1 for invalid sizes. `order` is the row order
+ * the select stage will be asked for: the score stage refuses a combination the select stage would refuse, because
+ * the score stage adds into `state`, which only a completed select stage clears. attnlab_select_lists checks its
+ * arguments again; called with other arguments than its score stage (another order, k or shape), it can refuse after
+ * the state was filled, and the caller must then zero the state itself. attnlab_sparse_decode_step takes the tiled
+ * select itself for score order with k > ATTNLAB_LDS_SORT_K.
  */
-int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k);
+int64_t attnlab_list_bytes(int B, int G, int lo, int hi, int k, int order);
 int attnlab_score_grouped_lists(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                                 const uint16_t* wq_t, float* u_out, float* out, int64_t out_stride, int B, int G,
-                                int r, int C, int d, int hd, int lo, int hi, int write_col, int k, uint32_t* state,
-                                void* lists, int64_t lists_bytes, void* stream);
+                                int r, int C, int d, int hd, int lo, int hi, int write_col, int k, int order,
+                                uint32_t* state, void* lists, int64_t lists_bytes, void* stream);
 int attnlab_select_lists(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
                          int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
                          const void* lists, int64_t lists_bytes, void* stream);

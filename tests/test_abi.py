@@ -128,15 +128,24 @@ def test_workspace_size_formula(native_lib):
 def test_list_bytes_formula(native_lib):
     for B, G, lo, hi, k in ((16, 8, 4, 32704, 1024), (1, 8, 4, 32704, 1024), (1, 8, 4, 1984, 64), (2, 8, 4, 300, 32),
                             (1, 8, 4, 32704, 16384), (1, 8, 0, 40000, 100), (4, 8, 60, 60, 0), (16, 8, 4, 16320, 512)):
-        assert native_lib.attnlab_list_bytes(B, G, lo, hi, k) == list_region(B * G, lo, hi, k)
-    assert native_lib.attnlab_list_bytes(0, 8, 0, 10, 1) == -1
-    assert native_lib.attnlab_list_bytes(1, 8, 0, 10, 11) == -1
+        assert native_lib.attnlab_list_bytes(B, G, lo, hi, k, 0) == list_region(B * G, lo, hi, k)
+        # score order: the list select sorts at most LDS_SORT_K picks
+        want = 0 if k > _native.LDS_SORT_K else list_region(B * G, lo, hi, k)
+        assert native_lib.attnlab_list_bytes(B, G, lo, hi, k, 1) == want
+    assert native_lib.attnlab_list_bytes(1, 8, 4, 32704, 9830, 0) > 0
+    assert native_lib.attnlab_list_bytes(1, 8, 4, 32704, 9830, 1) == 0
+    assert native_lib.attnlab_list_bytes(0, 8, 0, 10, 1, 0) == -1
+    assert native_lib.attnlab_list_bytes(1, 8, 0, 10, 11, 0) == -1
+    assert native_lib.attnlab_list_bytes(1, 8, 0, 10, 1, 2) == -1
 
 
 def test_list_select_refuses_shapes_it_does_not_cover(native_lib):
     with pytest.raises(ValueError, match="does not apply"):   # r = 16: not the one-launch score
         _native.call("attnlab_score_grouped_lists", *([16] * 7), 4096, 1, 8, 16, 4096, 128, 256, 4, 4000, 4095, 100,
-                     16, 256, 1 << 20, None)
+                     0, 16, 256, 1 << 20, None)
+    with pytest.raises(ValueError, match="score order"):      # score order past the LDS sort, before any launch
+        _native.call("attnlab_score_grouped_lists", *([16] * 7), 32768, 1, 8, 32, 32768, 128, 256, 4, 32704, 32767,
+                     9830, 1, 16, 256, 1 << 24, None)
     with pytest.raises(ValueError, match="does not apply"):   # M = 40000 > 32768
         _native.call("attnlab_select_lists", 16, 40000, 1, 8, 4, 40004, 40068, 100, 40100, 0, 16, 200, None, 16, 256,
                      1 << 20, None)

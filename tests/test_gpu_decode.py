@@ -33,13 +33,13 @@ def setup(gpu, B=1, G=8, h=2, C=2048 + 64, seed=0, r=32):
     return K, V, q, q_pre, k_pre_new, zT, idx
 
 
-def run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical, n0=None):
+def run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical, n0=None, workspace=None):
     B, G, C = K.shape[0], K.shape[1], K.shape[2]
     req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu, n0=n0)
     out, rows = sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo,
                                           req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count,
                                           k_pre_new=k_pre_new, write_col=req.write_col, return_rows=True,
-                                          canonical_order=canonical)
+                                          canonical_order=canonical, workspace=workspace)
     torch.cuda.synchronize()
     pos = (rows.view(B, G, -1) - req.offsets).cpu().numpy()
     return req, out, pos
@@ -70,12 +70,18 @@ def check_out(out, ref, what):
     (1, 2, 200, 128, 1 / 8, True),              # (68, 16, 84)
     (3, 1, 1000, 1000, 1 / 32, False),
     (1, 2, 32768 + 64, 32768, 1 / 2, False),    # score order past the LDS sort: k = 16384 (radix pass)
+    (1, 2, 32768 + 64, 32768, 0.3, False),      # k = 9830: past the LDS sort, inside the list select's k range
+    (2, 2, 16384 + 64, 16384, 0.55, False),     # k = 8974 of M = 16316
     (1, 2, 32768, 32768, 1.0, False),           # every candidate, score order: k = M = 32700
 ])
 def test_step_matches_oracle(gpu, B, h, C, L, rho, canonical):
+    from attention_lab import _native as nat
     K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L)
     zT_before = zT.clone()
-    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical)
+    ws = nat.Workspace()
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, zT, idx, L, rho, canonical, workspace=ws)
+    torch.cuda.synchronize()
+    assert int(ws.bytes(gpu, 0, "state").abs().sum()) == 0, "the step left its select state dirty"
     lo, hi, k, S = rules.step(L, req.k0)
     assert (req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count) == (lo, hi, k, S)
     assert pos.shape == (B, 8, S)
@@ -225,6 +231,62 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
+def test_graph_replay_survives_workspace_growth(gpu):
+    """A graph captured on a workspace, then a larger eager call that grows it: the retired buffers stay alive, so every
+    replay still equals the eager result of the captured shape, and the larger call is bit-exact against the oracle."""
+    from attention_lab import _native as nat
+    ws = nat.Workspace()
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=2, h=2, C=2048 + 64, seed=21)
+    L = 2048
+    req = prepare_request(2, 8, 2048 + 64, valid_length=L, query_position=L - 1, rho=1 / 32, device=gpu)
+    args = (q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo, req.layout.candidate_lo,
+            req.layout.candidate_hi, req.k, req.selected_count)
+    kw = dict(canonical_order=True, workspace=ws)
+    eager = sparse_decode_step_kernel(*args, **kw).clone()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        sparse_decode_step_kernel(*args, **kw)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured = sparse_decode_step_kernel(*args, **kw)
+    small = ws.bytes(gpu, 0, "step").numel()
+    # a larger eager step (B=4, 8K context) grows the workspace; torch may hand the retired memory to no one else
+    K2, V2, q2, q_pre2, k_new2, zT2, idx2 = setup(gpu, B=4, h=2, C=8192 + 64, seed=22)
+    _, out2, pos2 = run_step(gpu, K2, V2, q2, q_pre2, k_new2, zT2, idx2, 8192, 1 / 16, True, workspace=ws)
+    assert ws.bytes(gpu, 0, "step").numel() > small and ws.retired_bytes() >= small
+    lo2, hi2 = 4, 8192 - 64
+    s2 = kernel_scores(zT2, q_pre2, idx2, lo2, hi2)
+    assert np.array_equal(pos2, exact.select_rows(s2, lo2, hi2, 8192, pos2.shape[-1] - 68, order="position"))
+    filler = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=gpu) for _ in range(8)]   # reuse of freed memory
+    for _ in range(3):
+        captured.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), "a replay after the workspace grew differs from the eager result"
+        run_step(gpu, K2, V2, q2, q_pre2, k_new2, zT2.clone(), idx2, 8192, 1 / 16, False, workspace=ws)
+        torch.cuda.synchronize()
+    del filler
+    assert int(ws.bytes(gpu, 0, "state").abs().sum()) == 0
+
+
+def test_workspace_refuses_to_grow_under_capture(gpu):
+    from attention_lab import _native as nat
+    ws = nat.Workspace()
+    ws.bytes(gpu, 1024, "t")
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with pytest.raises(RuntimeError, match="capture"):
+            with torch.cuda.graph(g, stream=stream):
+                ws.bytes(gpu, 1 << 24, "t")
+    torch.cuda.synchronize()
+
+
 def test_rejected_call_leaves_the_select_state_clean(gpu):
     """A call the select rejects (an unknown row order) must fail before the score kernel adds its histogram into the
     shared select state: the next valid call's rows are still bit-exact against the oracle."""
@@ -352,7 +414,7 @@ def test_list_select_stages_through_the_abi(gpu, B, h, C, L, rho):
     req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
     lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
     M = hi - lo
-    nbytes = nat.lib().attnlab_list_bytes(B, G, lo, hi, k)
+    nbytes = nat.lib().attnlab_list_bytes(B, G, lo, hi, k, nat.ORDER_SCORE)
     assert nbytes > 0
     lists = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
     state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
@@ -366,7 +428,7 @@ def test_list_select_stages_through_the_abi(gpu, B, h, C, L, rho):
         rows = torch.empty(B * G, S, dtype=torch.int32, device=gpu)
         nat.call("attnlab_score_grouped_lists", z.data_ptr(), kn.data_ptr(), idx.wk.data_ptr(), qc.data_ptr(),
                  idx.wq_t_scaled.data_ptr(), None, scores.data_ptr(), M, B, G, 32, C, 128, h * 128, lo, hi, L - 1, k,
-                 state.data_ptr(), lists.data_ptr(), nbytes, stream)
+                 order, state.data_ptr(), lists.data_ptr(), nbytes, stream)
         nat.call("attnlab_select_lists", scores.data_ptr(), M, B, G, lo, hi, L, k, C, order, rows.data_ptr(), S, None,
                  state.data_ptr(), lists.data_ptr(), nbytes, stream)
         torch.cuda.synchronize()
@@ -406,3 +468,42 @@ def test_step_without_select_state(gpu):
         res.append((rows.cpu(), out.cpu()))
     assert int(state.abs().sum()) == 0
     assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+
+
+def test_list_stages_refuse_score_order_past_the_lds_sort(gpu):
+    """The list stages in score order past the LDS sort (k = 9830): attnlab_list_bytes gives 0 and the score stage
+    refuses before it touches the select state; in position order the same k runs, bit-exact against the oracle, and
+    leaves the state zero."""
+    from attention_lab import _native as nat
+    B, G, h, C, L = 1, 8, 2, 32768 + 64, 32768
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=77)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=0.3, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    assert k > nat.LDS_SORT_K
+    M = hi - lo
+    assert nat.lib().attnlab_list_bytes(B, G, lo, hi, k, nat.ORDER_SCORE) == 0
+    nbytes = nat.lib().attnlab_list_bytes(B, G, lo, hi, k, nat.ORDER_POSITION)
+    assert nbytes > 0, "the list select applies to this k in position order"
+    lists = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    qc = q_pre.reshape(B, G, h * 128).contiguous()
+    stream = nat.stream_of(gpu)
+    scores = torch.empty(B * G, M, dtype=torch.float32, device=gpu)
+    rows = torch.empty(B * G, S, dtype=torch.int32, device=gpu)
+
+    def score_stage(order):
+        nat.call("attnlab_score_grouped_lists", zT.data_ptr(), None, idx.wk.data_ptr(), qc.data_ptr(),
+                 idx.wq_t_scaled.data_ptr(), None, scores.data_ptr(), M, B, G, 32, C, 128, h * 128, lo, hi, L - 1, k,
+                 order, state.data_ptr(), lists.data_ptr(), nbytes, stream)
+
+    with pytest.raises(ValueError, match="score order"):
+        score_stage(nat.ORDER_SCORE)
+    torch.cuda.synchronize()
+    assert int(state.abs().sum()) == 0, "the refused score stage touched the state"
+    score_stage(nat.ORDER_POSITION)
+    nat.call("attnlab_select_lists", scores.data_ptr(), M, B, G, lo, hi, L, k, C, nat.ORDER_POSITION, rows.data_ptr(),
+             S, None, state.data_ptr(), lists.data_ptr(), nbytes, stream)
+    torch.cuda.synchronize()
+    assert int(state.abs().sum()) == 0
+    s = scores.view(B, G, M).cpu().numpy()
+    assert np.array_equal(rows.view(B, G, S).cpu().numpy(), exact.select_rows(s, lo, hi, L, k, order="position"))

@@ -97,3 +97,22 @@ def test_metal_module_reference_helpers():
     got = hip_attend.reference_attend(K, V, q, rows).numpy()
     want = exact.subset_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None], rows.numpy()[None].astype(np.int64))[0]
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_subset_attention_names_its_narrower_contract():
+    """subset_attention runs only on the HIP attend kernel (bfloat16, d = 128, h*T <= 8 query rows per group): other
+    inputs are refused up front with a ValueError that names the restriction, before any device work."""
+    from attention_lab.sparse import subset_attention
+    bf = torch.bfloat16
+    q, ks = torch.zeros(1, 2, 2, 1, 128, dtype=bf), torch.zeros(1, 2, 5, 128, dtype=bf)
+    with pytest.raises(ValueError, match="bfloat16 only; q is torch.float32"):
+        subset_attention(q.float(), ks, ks)
+    with pytest.raises(ValueError, match="bfloat16 only; k_sub is torch.float16"):
+        subset_attention(q, ks.half(), ks.half())
+    with pytest.raises(ValueError, match="head_dim 128 only, got 64"):
+        subset_attention(torch.zeros(1, 2, 2, 1, 64, dtype=bf), torch.zeros(1, 2, 5, 64, dtype=bf),
+                         torch.zeros(1, 2, 5, 64, dtype=bf))
+    with pytest.raises(ValueError, match="h\\*T <= 8 query rows per group, got 16"):
+        subset_attention(torch.zeros(1, 2, 8, 2, 128, dtype=bf), ks, ks, backend="explicit")
+    with pytest.raises(ValueError, match="unknown subset backend"):
+        subset_attention(q, ks, ks, backend="flash")
