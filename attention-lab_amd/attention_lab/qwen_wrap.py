@@ -298,56 +298,90 @@ _SELECTOR_IMPL = {"index": _IndexSelector, "recent": _RecentSelector, "uniform":
 # ---------------------------------------------------------------------------------------------------------------------
 # state
 # ---------------------------------------------------------------------------------------------------------------------
+def _read_config_layers(cache: LabCache, indexers, mode: str, selector: str, sparse_layers):
+    """Validate a read configuration against its cache and return the sparse layer set (None: every layer). The
+    messages are the contract's; this function's own rule is that a configuration is checked in full before any state
+    is built, cheapest property first."""
+    problems = []
+    if mode not in ("full", "sparse"):
+        problems.append("mode must be 'full' or 'sparse'")
+    if selector not in SELECTORS:
+        problems.append(f"selector must be one of {SELECTORS}")
+    if indexers is not None and len(indexers) != cache.layers:
+        problems.append("one indexer per layer")
+    if not problems and mode == "sparse" and selector == "index" and (indexers is None or not cache.has_index):
+        problems.append("the index selector (D0) needs indexers and a cache with an index table")
+    layers = None
+    if sparse_layers is not None:
+        layers = frozenset(int(x) for x in sparse_layers)
+        if any(not 0 <= x < cache.layers for x in layers):
+            problems.append("sparse layer index outside model")
+    if problems:
+        raise ValueError(problems[0])
+    return layers
+
+
+@dataclass
+class _RequestBudget:
+    """The budget of the request in flight. `number` counts the requests begun on a state, so the uniform selector's
+    draws differ between requests; `start_length` is the legal length of the request's first decode step."""
+    number: int = 0
+    rho: float | None = None
+    k0: int | None = None
+    start_length: int | None = None
+
+    def begin(self, valid_length: int, rho, k0) -> int:
+        self.number += 1
+        self.rho = None if rho is None else float(rho)
+        self.start_length = int(valid_length) + 1
+        self.k0 = fixed_budget(self.start_length, self.rho) if k0 is None else int(k0)
+        return self.k0
+
+
 class LabState:
     """One read configuration (reference qwen_wrap.py:189-256): the cache, the per-layer indexers, the mode (full or
-    sparse), the selector of a sparse read and the plan and phase of the forward in flight."""
+    sparse), the selector of a sparse read and the plan and phase of the forward in flight. The request's budget
+    (rho, k0, the first step's legal length, the request count) lives in a `_RequestBudget`; the reference's attribute
+    names read through to it."""
 
     def __init__(self, cache: LabCache, indexers=None, *, mode: str = "full", selector: str = "index",
                  decode_backend: str = "sdpa_fold", prefill_backend: str = "sdpa_fold", uniform_seed: int = 0,
                  sparse_layers=None, cache_guard=None, canonical_order=False):
-        if mode not in ("full", "sparse"):
-            raise ValueError("mode must be 'full' or 'sparse'")
-        if selector not in SELECTORS:
-            raise ValueError(f"selector must be one of {SELECTORS}")
-        if indexers is not None and len(indexers) != cache.layers:
-            raise ValueError("one indexer per layer")
-        if mode == "sparse" and selector == "index" and (indexers is None or not cache.has_index):
-            raise ValueError("the index selector (D0) needs indexers and a cache with an index table")
-        layers = None if sparse_layers is None else frozenset(int(x) for x in sparse_layers)
-        if layers is not None and not layers <= frozenset(range(cache.layers)):
-            raise ValueError("sparse layer index outside model")
-        self.cache, self.indexers, self.mode, self.selector = cache, indexers, mode, selector
-        self.sparse_layers = layers
+        self.sparse_layers = _read_config_layers(cache, indexers, mode, selector, sparse_layers)
+        self.cache, self.indexers = cache, indexers
+        self.mode, self.selector = mode, selector
+        self.selector_impl = _SELECTOR_IMPL[selector]()
         self.decode_backend, self.prefill_backend = decode_backend, prefill_backend
         self.uniform_seed = int(uniform_seed)
         self.cache_guard = cache_guard
         self.canonical_order = bool(canonical_order)
-        self.selector_impl = _SELECTOR_IMPL[selector]()
-        self.request_counter = 0          # bumped by begin_request, so C draws differently in each request
+        self.request = _RequestBudget()
         self.record_selection = False     # keep each layer's flat row list of the step in last_rows
         self.last_rows: list = [None] * cache.layers
         self.plan: StepPlan | None = None
         self.phase: str | None = None     # set by LabRunner before each forward, never inferred
-        self.rho = None
-        self.k0 = None
-        self.request_start_length = None
+
+    # the reference's names for the request budget
+    rho = property(lambda self: self.request.rho)
+    k0 = property(lambda self: self.request.k0)
+    request_start_length = property(lambda self: self.request.start_length)
+    request_counter = property(lambda self: self.request.number)
 
     def reads_sparse(self, layer: int) -> bool:
         return self.mode == "sparse" and (self.sparse_layers is None or layer in self.sparse_layers)
 
     def uniform_rng(self, step_index: int):
-        """C's generator for (seed, request, step): a step replayed after a rollback draws the same rows."""
+        """The uniform selector's generator for one step: PCG64 over the seed sequence (seed, request, step), so a
+        step replayed after a rollback draws the same rows and no two (request, step) pairs share a stream (the
+        reference's numpy default_rng([seed, request, step]), qwen_wrap.py:222-227)."""
         import numpy as np
-        return np.random.default_rng([self.uniform_seed, self.request_counter, int(step_index)])
+        seq = np.random.SeedSequence([self.uniform_seed, self.request.number, int(step_index)])
+        return np.random.Generator(np.random.PCG64(seq))
 
     def begin_request(self, rho: float, *, k0=None) -> int:
         """Fix k0 from the legal length of the request's first decode step (prefilled tokens + 1); an explicit k0
         overrides the rho rule (k0 = capacity selects every candidate, the sparse == full diagnostic)."""
-        self.rho = None if rho is None else float(rho)
-        self.request_start_length = self.cache.valid_length + 1
-        self.k0 = int(k0) if k0 is not None else fixed_budget(self.request_start_length, self.rho)
-        self.request_counter += 1
-        return self.k0
+        return self.request.begin(self.cache.valid_length, rho, k0)
 
 
 class StateHolder:
@@ -474,20 +508,25 @@ def _inner_attention(layer):
 
 
 def geometry_of(model) -> ModelGeometry:
-    """The attention geometry the config states, checked against the parameters' shapes."""
+    """The attention geometry the config states (reference qwen_wrap.py:351-366), checked against layer 0's parameter
+    shapes: a config edited after the weights were built is caught here, not inside a kernel."""
     cfg = model.config
     attn = _inner_attention(model.model.layers[0])
-    heads, groups, hidden = int(cfg.num_attention_heads), int(cfg.num_key_value_heads), int(cfg.hidden_size)
-    d = int(attn.head_dim)
-    for name, want in (("q_proj", (heads * d, hidden)), ("k_proj", (groups * d, hidden)),
-                       ("v_proj", (groups * d, hidden)), ("o_proj", (hidden, heads * d))):
-        got = tuple(getattr(attn, name).weight.shape)
-        if got != want:
-            raise ValueError(f"{name} weight shape {got} != {want} implied by the config")
-    if tuple(attn.q_norm.weight.shape) != (d,) or tuple(attn.k_norm.weight.shape) != (d,):
+    geo = ModelGeometry(layers=len(model.model.layers), hidden=int(cfg.hidden_size),
+                        heads=int(cfg.num_attention_heads), groups=int(cfg.num_key_value_heads),
+                        head_dim=int(attn.head_dim), vocab=int(cfg.vocab_size),
+                        max_positions=int(cfg.max_position_embeddings))
+    q_width, kv_width = geo.heads * geo.head_dim, geo.groups * geo.head_dim
+    implied = {"q_proj": (q_width, geo.hidden), "k_proj": (kv_width, geo.hidden), "v_proj": (kv_width, geo.hidden),
+               "o_proj": (geo.hidden, q_width)}
+    wrong = [(name, tuple(getattr(attn, name).weight.shape), want) for name, want in implied.items()
+             if tuple(getattr(attn, name).weight.shape) != want]
+    if wrong:
+        name, got, want = wrong[0]
+        raise ValueError(f"{name} weight shape {got} != {want} implied by the config")
+    if {tuple(attn.q_norm.weight.shape), tuple(attn.k_norm.weight.shape)} != {(geo.head_dim,)}:
         raise ValueError("q_norm / k_norm act on head_dim in Qwen3; shapes disagree")
-    return ModelGeometry(layers=len(model.model.layers), hidden=hidden, heads=heads, groups=groups, head_dim=d,
-                         vocab=int(cfg.vocab_size), max_positions=int(cfg.max_position_embeddings))
+    return geo
 
 
 def _param_device_dtype(model, device, dtype):
@@ -639,17 +678,28 @@ class NativeRunner:
         return self.forward(token_ids, logits_to_keep=1)
 
     def rollback(self, length: int) -> None:
-        removed = self.length - int(length)
-        if removed < 0:
+        """Make the cache hold the first `length` tokens again. Each layer is shortened by its own kind: a layer
+        preallocated to the capacity (transformers' static layer) keeps its storage and gets `length` as its written
+        count, so attention masks the slots past it; a growing layer (the dynamic one) is cut back to its first
+        `length` positions."""
+        length = int(length)
+        if length > self.length:
             raise ValueError("cannot roll forward")
-        if removed:
-            layers = self.cache.layers
-            if all(isinstance(getattr(lay, "cumulative_length", None), torch.Tensor) for lay in layers):
-                for lay in layers:   # static layers: slots past `length` fall outside the causal mask
-                    lay.cumulative_length.fill_(int(length))
-            else:
-                self.cache.crop(-removed)
-        self.length = int(length)
+        if length < self.length:
+            for lay in self.cache.layers:
+                _shorten_layer(lay, length)
+        self.length = length
+
+
+def _shorten_layer(lay, length: int) -> None:
+    written = getattr(lay, "cumulative_length", None)
+    if isinstance(written, torch.Tensor):
+        written.fill_(length)
+    elif isinstance(getattr(lay, "keys", None), torch.Tensor):
+        lay.keys = lay.keys[..., :length, :]
+        lay.values = lay.values[..., :length, :]
+    else:
+        raise TypeError(f"cannot roll back a cache layer of type {type(lay).__name__}")
 
 
 def tiny_qwen3(*, seed: int = 0, layers: int = 2, hidden: int = 64, heads: int = 4, groups: int = 2, head_dim: int = 16,

@@ -69,20 +69,29 @@ class FrozenBank:
         self._members = tuple(map(id, self.indexes))
 
     def guard(self, state):
-        """Run by LabRunner before a forward writes to the cache: the state still holds this bank's indexes, unedited
-        and on the cache's device, over a float32 index table that is empty or was filled by this bank."""
-        if tuple(map(id, state.indexers)) != self._members:
-            raise RuntimeError("state index bank changed")
+        """Run by LabRunner before a forward writes to the cache, then bind this bank's identity into the cache. The
+        rules, each with the contract's message: the table is a float32 index table; the state holds exactly this
+        bank's index objects; each is unedited and on the cache's device; a table that already holds keys was filled
+        by this bank."""
         cache = state.cache
-        for index in self.indexes:
-            index.verify()
-            if index.wk.device != cache.device:
-                raise RuntimeError("index/cache devices differ")
-        if not cache.has_index or cache.index_dtype != torch.float32:
-            raise RuntimeError("bank requires a float32 index cache")
-        if cache.valid_length and getattr(cache, "index_identity", None) != self.identity:
-            raise RuntimeError("prefix index cache belongs to different parameter identity")
+        for broken, message in self._rules(state, cache):
+            if broken():
+                raise RuntimeError(message)
         cache.index_identity = self.identity
+
+    def _rules(self, state, cache):
+        def edited():
+            for index in self.indexes:
+                index.verify()   # raises its own message
+            return False
+        return (
+            (lambda: not cache.has_index or cache.index_dtype != torch.float32, "bank requires a float32 index cache"),
+            (lambda: tuple(map(id, state.indexers or ())) != self._members, "state index bank changed"),
+            (edited, ""),
+            (lambda: any(index.wk.device != cache.device for index in self.indexes), "index/cache devices differ"),
+            (lambda: bool(cache.valid_length) and getattr(cache, "index_identity", None) != self.identity,
+             "prefix index cache belongs to different parameter identity"),
+        )
 
 
 @dataclass

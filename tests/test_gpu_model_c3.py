@@ -101,3 +101,70 @@ def test_configs3_qwen3_1p7b_8192_prompt(gpu):
         assert da_rel <= D_VS_A_REL, f"{order}: sparse (k0 = capacity) vs full read rel {da_rel:.3e}"
         print(f"[c3] {order}: vs float32 rel {d_rel:.3e} kl {d_kl:.3e}; vs full read rel {da_rel:.3e} "
               f"(full read vs float32 rel {a_rel:.3e} kl {a_kl:.3e})", flush=True)
+
+
+def test_configs3_partial_read_at_rho_1_32_touches_only_its_rows(gpu):
+    """configs[3] at its real budget: after the 8192-token prompt, one decode step at rho = 1/32 (k0 = 256 of 8125
+    candidates) in both row orders, with every layer's row list recorded. Each list holds S = 68 + k unique positions
+    inside the legal range, F among them ([0, 4) and the last 64), the candidates inside [lo, hi); position order is
+    strictly ascending, score order puts F first. Then every K/V row the step did not select is poisoned with NaN in
+    every layer (and every unwritten slot), the step is replayed after a rollback, and its logits are bit-identical to
+    the clean step while the dense read of the same cache turns non-finite (reference
+    tests/test_qwen_wrapper.py:150-208 at model scale)."""
+    from attention_lab.decode import dense_decode_step
+    from attention_lab.qwen_wrap import LabRunner, make_state, unwrap_model, wrap_model
+    from attention_lab.selection import fixed_budget
+    model = qwen3_1p7b(gpu, seed=1)
+    holder = wrap_model(model)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(1)
+    prompt = torch.randint(0, model.config.vocab_size, (1, PROMPT), device=gpu, generator=gen)
+    tok = torch.randint(0, model.config.vocab_size, (1, 1), device=gpu, generator=gen)
+    cap = PROMPT + 8
+    L = PROMPT + 1
+    lo, hi = 4, L - 64
+    with torch.inference_mode():
+        for canonical in (True, False):
+            st = make_state(model, cap, "sparse", canonical_order=canonical)
+            run = LabRunner(model, holder, st)
+            run.prefill(prompt, 2048)
+            assert st.begin_request(1 / 32) == fixed_budget(L, 1 / 32)
+            st.record_selection = True
+            clean = run.step(tok)
+            plan = st.plan
+            k, S = plan.k, plan.selected_count
+            assert (plan.legal_length, plan.lo, plan.hi, S) == (L, lo, hi, 68 + k) and k == st.k0 < hi - lo
+            cache = st.cache
+            G, C = cache.groups, cache.slots
+            fixed = torch.cat([torch.arange(4, device=gpu), torch.arange(L - 64, L, device=gpu)])
+            keep_all = []
+            for l in range(cache.layers):
+                rows = (st.last_rows[l].view(1, G, S) - cache.offsets)[0]
+                assert int(rows.min()) >= 0 and int(rows.max()) < L, f"layer {l}: a row outside the legal range"
+                srt = rows.sort(dim=-1).values
+                assert bool((srt[:, 1:] > srt[:, :-1]).all()), f"layer {l}: repeated rows"
+                assert bool(torch.isin(fixed, rows).all()), f"layer {l}: F missing from the row list"
+                if canonical:
+                    assert torch.equal(rows, srt), f"layer {l}: position order not ascending"
+                else:
+                    assert torch.equal(rows[:, :68], fixed.expand(G, 68)), f"layer {l}: score order must start with F"
+                    cand = rows[:, 68:]
+                    assert bool(((cand >= lo) & (cand < hi)).all()), f"layer {l}: a candidate outside [lo, hi)"
+                keep = torch.zeros(G, C, dtype=torch.bool, device=gpu)
+                keep.scatter_(1, rows.long(), True)
+                keep_all.append(keep)
+            for l in range(cache.layers):
+                drop = ~keep_all[l]
+                cache.k[l][0][drop] = float("nan")
+                cache.v[l][0][drop] = float("nan")
+            run.rollback(PROMPT)
+            poisoned = run.step(tok)
+            assert torch.isfinite(poisoned).all(), "the sparse read touched a row it did not select"
+            assert torch.equal(poisoned, clean), "poisoning unselected rows changed the sparse step's logits"
+            q = torch.randn(1, G, 2, 1, 128, device=gpu, generator=gen).to(torch.bfloat16)
+            dense = dense_decode_step(q, cache.k[0], cache.v[0], L)
+            assert not bool(torch.isfinite(dense.float()).all()), "the dense read must see the poison"
+            print(f"[c3] rho = 1/32, {'position' if canonical else 'score'} order: k = {k}, S = {S}, 28 layers, "
+                  "poisoned replay bit-identical", flush=True)
+            del run, st, cache, keep_all
+        unwrap_model(model)

@@ -350,3 +350,57 @@ def test_every_candidate_at_32k_in_either_row_order_equals_the_full_read(gpu, ca
                 assert torch.equal(rows[0, 0].cpu(), torch.arange(plan.legal_length))
             assert_close(d, a, TOL, f"step {i}: every candidate ({'position' if canonical else 'score'} order) vs full")
         unwrap_model(m)
+
+
+def test_a_sparse_step_runs_one_select_per_layer_and_no_dense_read(gpu, monkeypatch):
+    """The reference spies on a model step: one torch.topk per layer and no torch.gather in a sparse step, no top-k in
+    a full one (tests/test_qwen_wrapper.py:324-345), and its profiler check finds no full-length QK in the sparse read
+    (bench/microbench.py:207-229). Here every read is a C-ABI call, so the spy counts the entry points a step reaches:
+    a sparse step makes exactly one fused call per layer (its one select launch inside), and no dense decode, prefill,
+    standalone select, torch.topk, torch.gather or full_attention; a full step makes one dense decode per layer and no
+    sparse call. Both steps also rerun with the spy off and give the same logits."""
+    from attention_lab import _native as nat
+    from attention_lab import full as full_mod
+    from attention_lab import qwen_wrap
+    m, _ = tiny_pair(gpu, seed=6)
+    ids = token_ids(140, seed=6).to(gpu)
+    calls = []
+    real_call = nat.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return real_call(name, *args)
+
+    def refuse(*a, **k):
+        raise AssertionError("the sparse step took a dense read")
+
+    with torch.inference_mode():
+        holder = wrap_model(m)
+        st = make_state(m, 160, "sparse")
+        run = LabRunner(m, holder, st)
+        run.prefill(ids[:, :129], 129)
+        st.begin_request(1 / 8)
+        with monkeypatch.context() as mp:
+            mp.setattr(nat, "call", spy)
+            mp.setattr(qwen_wrap, "full_attention", refuse)
+            mp.setattr(full_mod, "full_attention", refuse)
+            mp.setattr(torch, "topk", lambda *a, **k: (_ for _ in ()).throw(AssertionError("torch.topk in a step")))
+            mp.setattr(torch, "gather", lambda *a, **k: (_ for _ in ()).throw(AssertionError("torch.gather in a step")))
+            spied = run.step(ids[:, 129:130])
+        layers = st.cache.layers
+        assert calls.count("attnlab_sparse_decode_step") == layers, calls
+        assert set(calls) == {"attnlab_sparse_decode_step"}, f"a sparse step reached {sorted(set(calls))}"
+        assert st.plan.selected_count < st.plan.legal_length, "the step must be a partial read"
+        run.rollback(129)
+        torch.testing.assert_close(run.step(ids[:, 129:130]), spied, rtol=0, atol=0)
+
+        calls.clear()
+        stA = make_state(m, 160, "full")
+        runA = LabRunner(m, holder, stA)
+        runA.prefill(ids[:, :129], 129)
+        with monkeypatch.context() as mp:
+            mp.setattr(nat, "call", spy)
+            runA.step(ids[:, 129:130])
+        assert calls.count("attnlab_dense_decode") == layers, calls
+        assert "attnlab_sparse_decode_step" not in calls and not any("select" in c or "topk" in c for c in calls)
+        unwrap_model(m)

@@ -155,3 +155,27 @@ def test_fixed_set_check_accepts_the_rule_and_refuses_anything_else():
     with pytest.raises(ValueError, match="selection rule"):                            # a different capacity
         check_standard_f(req.fixed_rows.clone(), req.off_lo.clone(), lo, hi, legal, 301)
     assert torch.equal(req.fixed_rows[1, 2], req.fixed_positions[1, 2] + (1 * 3 + 2) * 300)
+
+
+@pytest.mark.parametrize("kind", ["dynamic", "static"])
+def test_native_runner_rolls_back_either_cache_kind(kind):
+    """NativeRunner.rollback on transformers' growing (dynamic) and preallocated (static) caches: after rolling back
+    to 40 tokens, the replayed steps equal the first pass, and the cache reports 40 + replayed tokens."""
+    from transformers import DynamicCache, StaticCache
+    from attention_lab.qwen_wrap import NativeRunner
+    m = tiny_qwen3(seed=3)
+    ids = torch.randint(0, 256, (1, 52), generator=torch.Generator().manual_seed(4))
+    cache = DynamicCache(config=m.config) if kind == "dynamic" else StaticCache(config=m.config, max_cache_len=64)
+    with torch.inference_mode():
+        ref = m(ids).logits
+        run = NativeRunner(m, cache, 64)
+        run.prefill(ids[:, :40], 16)
+        first = torch.cat([run.step(ids[:, i:i + 1]) for i in range(40, 52)], 1)
+        torch.testing.assert_close(first, ref[:, 40:], rtol=1e-9, atol=1e-9)
+        run.rollback(40)
+        assert run.length == 40
+        with pytest.raises(ValueError):
+            run.rollback(41)
+        again = torch.cat([run.step(ids[:, i:i + 1]) for i in range(40, 52)], 1)
+        torch.testing.assert_close(again, first, rtol=0, atol=0)
+        assert int(cache.get_seq_length()) == 52
