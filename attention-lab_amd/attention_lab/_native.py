@@ -45,7 +45,7 @@ SIGNATURES = {
     "attnlab_select_scratch_bytes": (_i64, [_i] * 4),
     "attnlab_list_bytes": (_i64, [_i] * 6),
     "attnlab_score_grouped_lists": (_i, [_p] * 7 + [_i64] + [_i] * 11 + [_p, _p, _i64, _p]),
-    "attnlab_select_lists": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p]),
+    "attnlab_select_lists": (_i, [_p, _i64] + [_i] * 8 + [_p, _i64, _p, _p, _p, _i64, _p, _i, _p, _p]),
     "attnlab_attend": (_i, [_p, _p, _i64, _i, _p, _p, _i64] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_attend_paged": (_i, [_p, _p, _i, _i, _p, _i64, _i, _p, _p, _i64] + [_i] * 5 + [_f, _p, _i, _p, _p]),

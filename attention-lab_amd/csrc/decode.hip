@@ -57,7 +57,8 @@ template <typename Score>
 int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uint16_t* V, bool has_k_new, int B,
                             int G, int h, int C, int lo, int hi, int legal, int k, float scale, int order, int P,
                             uint32_t* state, void* workspace, int64_t workspace_bytes, int32_t* rows_out,
-                            int64_t* rows_flat, uint16_t* out, void* stream, attnlab::FusedGeometry geo, Score score) {
+                            int64_t* rows_flat, uint16_t* out, void* stream, attnlab::FusedGeometry geo,
+                            const void* zT, int z_dtype, Score score) {
     using namespace attnlab;
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && h >= 1 && h <= 8, "B=%d G=%d h=%d out of range", B, G, h);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
@@ -90,11 +91,16 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     // buffers
     const ListPlan plan = k > 0 && state && !staged_score_order(order, k) ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
     const ScoreLists lists = plan.cap > 0 ? list_layout(ws + L.sel, B * G, geo, plan) : ScoreLists{};
+    // Stored scores are read only by the tiled select and by score order (which reads the picks' scores back to sort
+    // them); the list select in position order recomputes the rare tile it needs from the table and u, so the score
+    // kernel then writes key lists only.
+    const bool store_scores = plan.cap == 0 || order == ATTNLAB_ORDER_SCORE;
+    float* u_ws = reinterpret_cast<float*>(ws + L.u);
     int rc;
     if (k > 0) {
         // u goes to the workspace (the score kernels that build it in-kernel also store it there)
-        rc = score(reinterpret_cast<float*>(ws + L.u), scores, L.score_stride, lo, hi, state,
-                   plan.cap > 0 ? &lists : nullptr, s);
+        rc = score(u_ws, store_scores ? scores : nullptr, L.score_stride, lo, hi, state, plan.cap > 0 ? &lists : nullptr,
+                   s);
     } else if (has_k_new) {
         // no candidate is read this step, but the newest key still gets its index column (empty scan range)
         rc = score(nullptr, nullptr, 0, lo, lo, nullptr, nullptr, s);
@@ -103,8 +109,8 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     }
     if (rc) return rc;
     if (plan.cap > 0)
-        rc = select_lists_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
-                               lists, geo, s);
+        rc = select_lists_impl(store_scores ? scores : nullptr, L.score_stride, B, G, lo, hi, legal, k, C, order, rows,
+                               S, rows_flat, state, lists, geo, s, TableRef{zT, z_dtype, C, u_ws});
     else
         rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
                               k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
@@ -123,7 +129,7 @@ extern "C" int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t
     return sparse_decode_step_impl(
         q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
         workspace_bytes, rows_out, rows_flat, out, stream,
-        attnlab::fused_geometry(B * G, C, r, h * 128, lo, hi, zT, false),
+        attnlab::fused_geometry(B * G, C, r, h * 128, lo, hi, zT, false), zT, ATTNLAB_DT_BF16,
         [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists* ls,
             hipStream_t s) {
             return attnlab::score_grouped_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r, C,
@@ -140,7 +146,7 @@ extern "C" int attnlab_sparse_decode_step_f32(const uint16_t* q_main, const floa
     return sparse_decode_step_impl(
         q_main, K, V, k_new != nullptr, B, G, h, C, lo, hi, legal, k, scale, order, P, state, workspace,
         workspace_bytes, rows_out, rows_flat, out, stream,
-        attnlab::fused_geometry_f32(B * G, C, r, h * 128, lo, hi, zT, wq_t, false),
+        attnlab::fused_geometry_f32(B * G, C, r, h * 128, lo, hi, zT, wq_t, false), zT, ATTNLAB_DT_F32,
         [&](float* u_ws, float* scores, int64_t stride, int slo, int shi, uint32_t* st, const attnlab::ScoreLists* ls,
             hipStream_t s) {
             return attnlab::score_grouped_f32_impl(zT, k_new, wk, q_cat, wq_t, nullptr, u_ws, scores, stride, B, G, r,

@@ -369,7 +369,9 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     if (tid < 2) lcount[tid] = 0u;
     __syncthreads();
 
-    float* o = a.out + (size_t)bg * a.out_stride - lo;
+    // a.out null (key lists only, the fused step's position order): no score is stored; the list select recomputes
+    // the few tiles it needs from the table
+    float* o = a.out ? a.out + (size_t)bg * a.out_stride - lo : nullptr;
     uint32_t lkey[2 * NSUB];   // this thread's keys (columns cb0 + s * sstride + 2 tid + e), kept for the list
     uint32_t lvalid = 0u;
 #pragma unroll
@@ -379,16 +381,17 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         float acc[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+        // explicit fma chains from zero in row order: rescore8 (the select's recompute) repeats them bit for bit
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-            acc[0] += u[jj] * bf16_lo(v[jj].x);
-            acc[1] += u[jj] * bf16_hi(v[jj].x);
-            acc[2] += u[jj] * bf16_lo(v[jj].y);
-            acc[3] += u[jj] * bf16_hi(v[jj].y);
-            acc[4] += u[jj] * bf16_lo(v[jj].z);
-            acc[5] += u[jj] * bf16_hi(v[jj].z);
-            acc[6] += u[jj] * bf16_lo(v[jj].w);
-            acc[7] += u[jj] * bf16_hi(v[jj].w);
+            acc[0] = __builtin_fmaf(u[jj], bf16_lo(v[jj].x), acc[0]);
+            acc[1] = __builtin_fmaf(u[jj], bf16_hi(v[jj].x), acc[1]);
+            acc[2] = __builtin_fmaf(u[jj], bf16_lo(v[jj].y), acc[2]);
+            acc[3] = __builtin_fmaf(u[jj], bf16_hi(v[jj].y), acc[3]);
+            acc[4] = __builtin_fmaf(u[jj], bf16_lo(v[jj].z), acc[4]);
+            acc[5] = __builtin_fmaf(u[jj], bf16_hi(v[jj].z), acc[5]);
+            acc[6] = __builtin_fmaf(u[jj], bf16_lo(v[jj].w), acc[6]);
+            acc[7] = __builtin_fmaf(u[jj], bf16_hi(v[jj].w), acc[7]);
         }
         float4* pw = reinterpret_cast<float4*>(&part[wave][lane * 8]);
         pw[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -404,12 +407,12 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         lkey[2 * s] = score_key(s0);
         lkey[2 * s + 1] = score_key(s1);
         if (c >= lo && c < hi) {
-            o[c] = s0;
+            if (o) o[c] = s0;
             lvalid |= 1u << (2 * s);
             if (a.hist) atomicAdd(&hsh[lkey[2 * s] >> kHistShift], 1u);
         }
         if (c + 1 >= lo && c + 1 < hi) {
-            o[c + 1] = s1;
+            if (o) o[c + 1] = s1;
             lvalid |= 2u << (2 * s);
             if (a.hist) atomicAdd(&hsh[lkey[2 * s + 1] >> kHistShift], 1u);
         }
@@ -777,7 +780,8 @@ int attnlab::score_grouped_impl(uint16_t* zT, const uint16_t* k_new, const uint1
                         write_col, lo, hi);
     }
     const int M = hi - lo;
-    ATTNLAB_REQUIRE(M == 0 || (out != nullptr && out_stride >= M), "out must hold M=%d scores per row", M);
+    ATTNLAB_REQUIRE(M == 0 || (out != nullptr && out_stride >= M) || (out == nullptr && lists != nullptr),
+                    "out must hold M=%d scores per row", M);
     ScoreArgs a{zT, k_new, wk, q_cat, wq_t, u_in, u_out, out, out_stride, G, r, C, d, hd, lo, M, write_col, 1, hist,
                 ScoreLists{nullptr, nullptr, 0, 0}};
     const bool vec = vector && (C % 4 == 0) && (reinterpret_cast<uintptr_t>(zT) % 8 == 0);

@@ -255,7 +255,7 @@ __global__ __launch_bounds__(256) void score_scan_fused_f32(ScoreF32Args a) {
     if (tid < 2) lcount[tid] = 0u;
     __syncthreads();
 
-    float* o = a.out + (size_t)bg * a.out_stride - lo;
+    float* o = a.out ? a.out + (size_t)bg * a.out_stride - lo : nullptr;   // null: key lists only
     uint32_t lkey[2 * NSUB];   // this thread's keys (columns cb0 + s * sstride + 2 tid + e), kept for the list
     uint32_t lvalid = 0u;
 #pragma unroll
@@ -265,10 +265,11 @@ __global__ __launch_bounds__(256) void score_scan_fused_f32(ScoreF32Args a) {
         float acc[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+        // explicit fma chains from zero in row order: rescore8 (the select's recompute) repeats them bit for bit
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] += u[jj] * v[2 * jj + (i >> 2)][i & 3];
+            for (int i = 0; i < 8; ++i) acc[i] = __builtin_fmaf(u[jj], v[2 * jj + (i >> 2)][i & 3], acc[i]);
         *reinterpret_cast<float4*>(&part[wave][lane * 4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         *reinterpret_cast<float4*>(&part[wave][256 + lane * 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
         __syncthreads();
@@ -282,12 +283,12 @@ __global__ __launch_bounds__(256) void score_scan_fused_f32(ScoreF32Args a) {
         lkey[2 * s] = score_key(s0);
         lkey[2 * s + 1] = score_key(s1);
         if (c >= lo && c < hi) {
-            o[c] = s0;
+            if (o) o[c] = s0;
             lvalid |= 1u << (2 * s);
             if (a.hist) atomicAdd(&hsh[lkey[2 * s] >> kHistShift], 1u);
         }
         if (c + 1 >= lo && c + 1 < hi) {
-            o[c + 1] = s1;
+            if (o) o[c + 1] = s1;
             lvalid |= 2u << (2 * s);
             if (a.hist) atomicAdd(&hsh[lkey[2 * s + 1] >> kHistShift], 1u);
         }
@@ -504,7 +505,8 @@ int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const
     const bool need_u = !u_in && u_out;   // the prologue projects the query whenever u_out is given without u_in
     if (need_u) ATTNLAB_REQUIRE(q_cat && wq_t && hd >= 1, "computing u needs q_cat, wq_t and hd >= 1");
     if (M > 0) {
-        ATTNLAB_REQUIRE(out != nullptr && out_stride >= M, "out must hold M=%d scores per row", M);
+        ATTNLAB_REQUIRE((out != nullptr && out_stride >= M) || (out == nullptr && lists != nullptr),
+                        "out must hold M=%d scores per row", M);
         ATTNLAB_REQUIRE(u_in || u_out, "give u_in, or q_cat, wq_t and a u_out buffer for the prologue");
     }
     const int BG = B * G;

@@ -89,6 +89,94 @@ __device__ __forceinline__ uint32_t wave_digit_of_rank(const uint32_t* hist, uin
     return (uint32_t)(hib - (__ffsll((unsigned long long)m2) - 1));
 }
 
+// The index table a row's candidate scores come from, for the select of the fused step when the score kernel wrote
+// only key lists: zT [B*G, 32, C] (bf16 or float32, C % 8 == 0, 16-byte aligned) and u [B*G, 32] as the score kernel
+// built and stored it.
+struct TableRef {
+    const void* zT;
+    int dtype;   // ATTNLAB_DT_BF16 or ATTNLAB_DT_F32
+    int C;
+    const float* u;
+};
+
+// Scores of index-table columns c0 .. c0 + 7 (c0 % 8 == 0, c0 + 8 <= C) of row bg, in the exact fp32 operation order
+// of the one-launch score kernels (score_scan_fused, score_scan_fused_f32): for each group of eight index rows
+// j in [8w, 8w + 8), an fma chain from zero in row order, then (p0 + p1) + (p2 + p3). A key recomputed here is
+// therefore bit for bit the key those kernels counted in the histogram and put in the lists.
+// One group of eight index rows (wave w of the score kernel): p[i] = fma chain over j in [8w, 8w + 8) of
+// u[j] * z[j][c0 + i], from zero in row order. T: uint16_t (bf16 table) or float.
+template <typename T>
+__device__ __forceinline__ void rescore_rows8(const TableRef& t, int bg, int c0, int w, float (&p)[8]) {
+    const float* u = t.u + (size_t)bg * 32 + 8 * w;
+    const T* zr = static_cast<const T*>(t.zT) + ((size_t)bg * 32 + 8 * w) * (size_t)t.C + c0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+        float z[8];
+        if constexpr (sizeof(T) == 4) {
+            const float4* src = reinterpret_cast<const float4*>(zr + (size_t)jj * t.C);
+            const float4 a = src[0], b = src[1];
+            z[0] = a.x; z[1] = a.y; z[2] = a.z; z[3] = a.w;
+            z[4] = b.x; z[5] = b.y; z[6] = b.z; z[7] = b.w;
+        } else {
+            const uint4 v = *reinterpret_cast<const uint4*>(zr + (size_t)jj * t.C);
+            z[0] = bf16_lo(v.x); z[1] = bf16_hi(v.x); z[2] = bf16_lo(v.y); z[3] = bf16_hi(v.y);
+            z[4] = bf16_lo(v.z); z[5] = bf16_hi(v.z); z[6] = bf16_lo(v.w); z[7] = bf16_hi(v.w);
+        }
+        const float uj = u[jj];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = __builtin_fmaf(uj, z[i], p[i]);
+    }
+}
+
+// Rare paths (a tile whose list is incomplete, a row resolved by radix passes): each group of eight index rows is
+// loaded and reduced before the next is issued (scheduling barriers), which keeps this off the select's register
+// budget.
+template <typename T>
+__device__ __forceinline__ void rescore8_t(const TableRef& t, int bg, int c0, float (&s)[8]) {
+    float a[8], b[8];
+    rescore_rows8<T>(t, bg, c0, 0, a);
+    __builtin_amdgcn_sched_barrier(0);
+    rescore_rows8<T>(t, bg, c0, 1, b);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = a[i] + b[i];   // p0 + p1
+    float c[8];
+    rescore_rows8<T>(t, bg, c0, 2, b);
+    __builtin_amdgcn_sched_barrier(0);
+    rescore_rows8<T>(t, bg, c0, 3, c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = a[i] + (b[i] + c[i]);   // (p0 + p1) + (p2 + p3)
+}
+
+__device__ __forceinline__ void rescore8(const TableRef& t, int bg, int c0, float (&s)[8]) {
+    if (t.dtype == ATTNLAB_DT_F32) rescore8_t<float>(t, bg, c0, s);
+    else rescore8_t<uint16_t>(t, bg, c0, s);
+}
+
+// A row's candidate scores for the select: read from the stored scores where the score stage wrote them (srow,
+// candidate index m at srow[m]), else recomputed from the index table. group8 gives table columns c0 .. c0 + 7
+// (c0 % 8 == 0); entries outside [lo, hi) are 0 and must be masked by the caller.
+struct RowScores {
+    const float* srow;
+    TableRef table;
+    int bg, lo, hi;
+
+    __device__ __forceinline__ void group8(int c0, float (&s)[8]) const {
+        if (srow) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = c0 + i;
+                s[i] = c >= lo && c < hi ? srow[c - lo] : 0.0f;
+            }
+        } else {
+            rescore8(table, bg, c0, s);
+        }
+    }
+};
+
 // Per-workgroup key lists of the fused decode step (the score kernel writes them, the list select reads them): for
 // each score workgroup of a row, every key of its tile whose first digit is at least the digit of its lmin-th largest
 // key, as (candidate index, key) pairs, and a header (that digit, the list's length; a length above cap means the
@@ -137,8 +225,9 @@ __device__ __forceinline__ void write_key_list(const ScoreLists& L, const uint32
 
 // The argument checks of attnlab_select_rows (the decode step runs them before its first launch, so a rejected call
 // leaves the select state untouched).
+// scores_needed = false: the select recomputes its scores from the index table (the list select of the fused step).
 int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
-                 int64_t rows_stride, const float* scores, int64_t score_stride);
+                 int64_t rows_stride, const float* scores, int64_t score_stride, bool scores_needed = true);
 
 // attnlab_select_rows: `state` [B*G][kSelectStateWords] (nullable) holds the first-digit histograms the score kernel
 // built; with it and a scratch of select_scratch_bytes(B*G, M, k, order) the select runs tiled over the chip.
@@ -218,9 +307,12 @@ inline ScoreLists list_layout(void* base, int R, FusedGeometry g, ListPlan p) {
 
 // The list select of the fused decode step: from the score kernel's per-workgroup lists (and the full tile scores of
 // any list that cannot hold the row's selection), the top-k and F as attnlab_select_rows writes them; one launch.
+// scores may be null when `table` is given (its zT and u): the select then recomputes the scores of a tile whose list
+// is incomplete (and of a row resolved by radix passes) from the table, bit-exact; position order only, since score
+// order reads the selected keys' scores back.
 int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
                       int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
-                      const ScoreLists& lists, FusedGeometry geo, hipStream_t stream);
+                      const ScoreLists& lists, FusedGeometry geo, hipStream_t stream, TableRef table = TableRef{});
 
 // attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,

@@ -1450,6 +1450,7 @@ struct ListArgs {
     const uint2* entries;   // [R, tiles, cap]
     const uint2* hdr;       // [R, tiles]
     int cap, tiles, nsub, lspl;
+    TableRef table;         // where SelectArgs::scores is null: the table the scores are recomputed from
 };
 
 template <int MAXSUB>
@@ -1473,7 +1474,7 @@ __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListAr
     L.misc = misc;
     L.wave_tot = sh.wave_tot;
     ListRow r;
-    r.srow = a.scores + (size_t)row * a.score_stride;
+    r.scores = RowScores{a.scores ? a.scores + (size_t)row * a.score_stride : nullptr, t.table, row, a.lo, a.hi};
     r.state = a.hist + (size_t)row * kSelectStateWords;
     r.entries = t.entries + (size_t)row * t.tiles * t.cap;
     r.hdr = t.hdr + (size_t)row * t.tiles;
@@ -1684,7 +1685,7 @@ static int run_select(const SelectArgs& a, int R, bool tiled, void* scratch, hip
 }
 
 int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int order, const int32_t* rows,
-                 int64_t rows_stride, const float* scores, int64_t score_stride) {
+                 int64_t rows_stride, const float* scores, int64_t score_stride, bool scores_needed) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1, "B and G must be positive (B=%d G=%d)", B, G);
     ATTNLAB_REQUIRE(0 <= lo && lo <= hi && hi <= legal && legal <= C, "need 0 <= lo <= hi <= legal <= C, got %d %d %d %d",
                     lo, hi, legal, C);
@@ -1694,14 +1695,22 @@ int select_check(int B, int G, int lo, int hi, int legal, int k, int C, int orde
     const int S = lo + (legal - hi) + k;
     ATTNLAB_REQUIRE(S >= 1, "empty row list");
     ATTNLAB_REQUIRE(rows == nullptr || rows_stride >= S, "rows_stride=%lld smaller than S=%d", (long long)rows_stride, S);
-    ATTNLAB_REQUIRE(k == 0 || (scores != nullptr && score_stride >= M), "scores must hold M=%d values per row", M);
+    ATTNLAB_REQUIRE(k == 0 || !scores_needed || (scores != nullptr && score_stride >= M),
+                    "scores must hold M=%d values per row", M);
     return ATTNLAB_OK;
 }
 
 int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
                       int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
-                      const ScoreLists& lists, FusedGeometry geo, hipStream_t stream) {
-    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride);
+                      const ScoreLists& lists, FusedGeometry geo, hipStream_t stream, TableRef table) {
+    // without stored scores: the table they are recomputed from; position order (score order reads them back)
+    const bool recompute = scores == nullptr;
+    ATTNLAB_REQUIRE(!recompute || (table.zT != nullptr && table.u != nullptr && table.C % 8 == 0 && hi <= table.C &&
+                                   (table.dtype == ATTNLAB_DT_BF16 || table.dtype == ATTNLAB_DT_F32) &&
+                                   (reinterpret_cast<uintptr_t>(table.zT) & 15) == 0 &&
+                                   order == ATTNLAB_ORDER_POSITION),
+                    "the list select without stored scores needs the aligned index table, u and position order");
+    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride, !recompute);
     if (rc) return rc;
     const int M = hi - lo;
     ATTNLAB_REQUIRE(k > 0 && M <= kListMaxM && geo.nsub >= 1 && geo.nsub <= 8 && geo.tiles >= 1 &&
@@ -1713,7 +1722,8 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
                     "the list select needs the select state and the lists");
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
-    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots)};
+    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots),
+               recompute ? table : TableRef{}};
     // the instance for up to four sub-tiles per score workgroup keeps fewer registers live
     if (geo.nsub <= 4) hipLaunchKernelGGL(select_lists<4>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
     else hipLaunchKernelGGL(select_lists<8>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
@@ -1797,8 +1807,9 @@ extern "C" int attnlab_select_rows(const float* scores, int64_t score_stride, in
 
 extern "C" int attnlab_select_lists(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal,
                                     int k, int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat,
-                                    uint32_t* state, const void* lists, int64_t lists_bytes, void* stream) {
-    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride);
+                                    uint32_t* state, const void* lists, int64_t lists_bytes, const void* zT,
+                                    int z_dtype, const float* u, void* stream) {
+    int rc = select_check(B, G, lo, hi, legal, k, C, order, rows, rows_stride, scores, score_stride, scores != nullptr);
     if (rc) return rc;
     const FusedGeometry geo = fused_tiling(B * G, lo, hi);
     const ListPlan plan = hi > lo ? list_plan(hi - lo, k, geo) : ListPlan{0, 0};
@@ -1811,9 +1822,10 @@ extern "C" int attnlab_select_lists(const float* scores, int64_t score_stride, i
                         lists_bytes >= list_bytes(B * G, geo, plan),
                     "lists must be 256-byte aligned and hold attnlab_list_bytes = %lld bytes",
                     (long long)list_bytes(B * G, geo, plan));
+    const TableRef table = scores ? TableRef{} : TableRef{zT, z_dtype, C, u};
     return select_lists_impl(scores, score_stride, B, G, lo, hi, legal, k, C, order, rows, rows_stride, rows_flat,
                              state, list_layout(const_cast<void*>(lists), B * G, geo, plan), geo,
-                             reinterpret_cast<hipStream_t>(stream));
+                             reinterpret_cast<hipStream_t>(stream), table);
 }
 
 extern "C" int64_t attnlab_select_scratch_bytes(int R, int M, int k, int order) {

@@ -14,7 +14,9 @@
 //   3. finds the second digit; when its bin holds exactly the keys still to take (the usual case) the selection is
 //      complete, else a third digit and the first krem tied keys in index order (a tie bitmap and one block scan).
 // A bin b1 holding more than kListCandCap keys is resolved by three radix passes over the row's scores instead. The
-// result is the selection bitmap in LDS (bit i: candidate i is among the top k; ties go to the lower index).
+// scores of an incomplete list's tile and of a radix-resolved row are the stored ones where the score stage wrote them,
+// else recomputed from the index table in the score kernel's exact operation order (rescore8). The result is the
+// selection bitmap in LDS (bit i: candidate i is among the top k; ties go to the lower index).
 #pragma once
 
 #include "common.h"
@@ -28,7 +30,7 @@ constexpr int kListWords = kListMaxM / 32;            // selection bitmap words:
 // One row of the list select. The score kernel's tiling (nsub sub-tiles of 512 columns per workgroup, tiles
 // workgroups) locates an incomplete list's scores.
 struct ListRow {
-    const float* srow;        // the row's M candidate scores
+    RowScores scores;         // the row's M candidate scores (stored, or recomputed from the index table)
     const uint32_t* state;    // the row's select state (first-digit bins, then super-bins)
     const uint2* entries;     // the row's lists [tiles, cap]
     const uint2* hdr;         // [tiles] (d_L, length)
@@ -158,50 +160,45 @@ __device__ __forceinline__ void take_ties(const ListLds& L, uint32_t krem) {
 }
 
 // Bin b1 too full for the candidate array: the remaining two digits by passes over the row's scores, then every key
-// above the threshold and the first krem keys equal to it. Called by every thread with the same b1 and krem.
+// above the threshold and the first krem keys equal to it. Called by every thread with the same b1 and krem. The three
+// passes are one loop (pass 0: second digit of bin b1's keys; pass 1: third digit of prefix p2; pass 2: keys above
+// and equal to the threshold T into the two bitmaps), so the score read, possibly a recompute from the table, is
+// emitted once.
 template <int THREADS>
 __device__ __forceinline__ void radix_bitmap(const ListRow& r, const ListLds& L, uint32_t b1, uint32_t krem) {
-    constexpr int W = kListWords / THREADS;
     const int tid = threadIdx.x;
-    const int M = r.M;
-    for (int i = tid * 4; i < M; i += THREADS * 4)
+    uint32_t prefix = b1;   // pass 0: the first digit; pass 1: the first two (p2); pass 2: the threshold key T
+#pragma unroll 1
+    for (int pass = 0; pass < 3; ++pass) {
+        for (int c0 = (r.lo & ~7) + 8 * tid; c0 < r.hi; c0 += 8 * THREADS) {
+            float v[8];
+            r.scores.group8(c0, v);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (i + e >= M) break;
-            const uint32_t key = score_key(r.srow[i + e]);
-            if ((key >> kHistShift) == b1) atomicAdd(&L.hist2[(key >> 10) & 2047u], 1u);
+            for (int i = 0; i < 8; ++i) {
+                const int c = c0 + i;
+                if (c < r.lo || c >= r.hi) continue;
+                const uint32_t key = score_key(v[i]), m = (uint32_t)(c - r.lo);
+                if (pass == 0) {
+                    if ((key >> kHistShift) == prefix) atomicAdd(&L.hist2[(key >> 10) & 2047u], 1u);
+                } else if (pass == 1) {
+                    if ((key >> 10) == prefix) atomicAdd(&L.hist3[key & 1023u], 1u);
+                } else if (key > prefix) {   // both bitmaps start zeroed (the first round trip cleared them)
+                    atomicOr(&L.bits[m >> 5], 1u << (m & 31u));
+                } else if (key == prefix) {
+                    atomicOr(&L.ties[m >> 5], 1u << (m & 31u));
+                }
+            }
         }
-    __syncthreads();
-    wave0_find_digit(L.misc + 1, L.hist2, krem, 2048);
-    const uint32_t p2 = (b1 << 11) | (L.misc[1] & 2047u);
-    krem = L.misc[2];
-    for (int i = tid * 4; i < M; i += THREADS * 4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (i + e >= M) break;
-            const uint32_t key = score_key(r.srow[i + e]);
-            if ((key >> 10) == p2) atomicAdd(&L.hist3[key & 1023u], 1u);
+        __syncthreads();
+        if (pass == 0) {
+            wave0_find_digit(L.misc + 1, L.hist2, krem, 2048);
+            prefix = (b1 << 11) | (L.misc[1] & 2047u);
+        } else if (pass == 1) {
+            wave0_find_digit(L.misc + 1, L.hist3, krem, 1024);
+            prefix = (prefix << 10) | (L.misc[1] & 1023u);
         }
-    __syncthreads();
-    wave0_find_digit(L.misc + 1, L.hist3, krem, 1024);
-    const uint32_t T = (p2 << 10) | (L.misc[1] & 1023u);
-    krem = L.misc[2];
-    // thread t classifies the 32 W keys of its words
-#pragma unroll
-    for (int i = 0; i < W; ++i) {
-        const int w = tid * W + i;
-        uint32_t gt = 0u, eq = 0u;
-        for (int b = 0; b < 32; ++b) {
-            const int idx = 32 * w + b;
-            if (idx >= M) break;
-            const uint32_t key = score_key(r.srow[idx]);
-            gt |= (uint32_t)(key > T) << b;
-            eq |= (uint32_t)(key == T) << b;
-        }
-        L.bits[w] = gt;
-        L.ties[w] = eq;
+        krem = pass < 2 ? L.misc[2] : krem;
     }
-    __syncthreads();
     take_ties<THREADS>(L, krem);
 }
 
@@ -323,9 +320,12 @@ __device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListL
                 }
                 take(idx, key, ok, 8);
             }
+        } else if (!r.scores.srow) {
+            // an incomplete list whose scores were not stored: its tile is recomputed by every thread below
         } else {
-            // an incomplete list: the tile's scores, lane -> 8 consecutive columns of each sub-tile, four sub-tiles'
-            // loads issued before the first is used
+            // an incomplete list: the tile's stored scores, lane -> 8 consecutive columns of each sub-tile, four
+            // sub-tiles' loads issued before the first is used
+            const float* srow = r.scores.srow;
             const int cb = (r.lo & ~7) + w * 512 + lane * 8;
 #pragma unroll
             for (int sb = 0; sb < MAXSUB; sb += 4) {
@@ -336,7 +336,7 @@ __device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListL
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const int c = cb + (sb + s) * nt * 512 + i;
-                        v[s][i] = sb + s < r.nsub && c >= r.lo && c < r.hi ? r.srow[c - r.lo] : 0.0f;
+                        v[s][i] = sb + s < r.nsub && c >= r.lo && c < r.hi ? srow[c - r.lo] : 0.0f;
                     }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
@@ -352,6 +352,51 @@ __device__ __forceinline__ void list_select_bitmap(const ListRow& r, const ListL
                     take(idx, key, ok, 8);
                 }
             }
+        }
+    }
+    if (!r.scores.srow) {
+        // The tiles of the incomplete lists, recomputed from the index table by the whole workgroup: a wave takes 64
+        // groups of 8 columns at a time (group q: list = the (q / (64 nsub))-th incomplete one, sub-tile
+        // (q / 64) % nsub, columns 8 (q % 64) .. + 8 of it). Every wave reads the same headers, so the lists agree.
+        const uint2 h0 = lane < nt ? L.hdr[lane] : make_uint2(0u, 0u);
+        const uint2 h1 = lane + 64 < nt ? L.hdr[lane + 64] : make_uint2(0u, 0u);
+        const uint64_t f0 = __ballot(lane < nt && (h0.x > b1 || h0.y > (uint32_t)r.cap));
+        const uint64_t f1 = __ballot(lane + 64 < nt && (h1.x > b1 || h1.y > (uint32_t)r.cap));
+        const int nf = __popcll(f0) + __popcll(f1);
+        const int items = nf * r.nsub * 64;
+        for (int q0 = 64 * wave; q0 < items; q0 += 64 * kWaves) {
+            const int q = q0 + lane;
+            float v[8];
+            int c0 = 0;
+            if (q < items) {
+                int nth = q / (64 * r.nsub);   // the nth incomplete list (its number: the nth set bit of f0, f1)
+                uint64_t m = f0;
+                int base = 0;
+                if (nth >= __popcll(f0)) {
+                    nth -= __popcll(f0);
+                    m = f1;
+                    base = 64;
+                }
+                for (; nth > 0; --nth) m &= m - 1;
+                const int wl = base + __ffsll((unsigned long long)m) - 1;
+                const int sb = (q / 64) % r.nsub;
+                c0 = (r.lo & ~7) + (sb * nt + wl) * 512 + (q % 64) * 8;
+            }
+            if (q < items && c0 < r.hi) {
+                r.scores.group8(c0, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+            }
+            uint32_t idx[8], key[8], ok = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = c0 + i;
+                key[i] = score_key(v[i]);
+                idx[i] = (uint32_t)(c - r.lo);
+                ok |= (uint32_t)(q < items && c >= r.lo && c < r.hi) << i;
+            }
+            take(idx, key, ok, 8);
         }
     }
     __syncthreads();

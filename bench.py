@@ -142,9 +142,10 @@ def pmc_workload(torch, dev, args):
     torch.cuda.synchronize()
     print(json.dumps({"pmc_workload": f"{'score + select' if args.pmc_workload == 'select' else SCAN_KERNEL} x5 then "
                                       f"256 MiB copy x5", "select_algorithmic_bytes": ls.select_bytes(),
-                      "scores_bytes": ls.B * ls.G * 4 * ls.M, "scan_algorithmic_bytes": ls.score_bytes(),
-                      "scan_read_bytes": ls.score_bytes() - ls.B * ls.G * (4 * ls.M + 2 * ls.r),
-                      "scan_write_bytes": ls.B * ls.G * (4 * ls.M + 2 * ls.r),
+                      "scores_bytes": 0 if ls.lists_only else ls.B * ls.G * 4 * ls.M,
+                      "scan_algorithmic_bytes": ls.score_bytes(),
+                      "scan_read_bytes": ls.score_bytes() - ls.B * ls.G * ls.score_write_bytes(),
+                      "scan_write_bytes": ls.B * ls.G * ls.score_write_bytes(),
                       "copy_bytes_each_way": PMC_COPY_BYTES}))
     return 0
 
@@ -268,16 +269,26 @@ class LayerStack:
         self.dense_out = [torch.empty(B, G, h, d, device=dev, dtype=bf) for _ in range(layers)]
         self.scores = torch.empty(B, G, (self.M + 3) // 4 * 4, device=dev, dtype=torch.float32)
         self.rows = torch.empty(B, G, self.S, device=dev, dtype=torch.int32)
+        # the step (position order) stores no score where the list select applies: the score kernel writes key lists
+        # only and the select recomputes the rare tile it needs from the table; elsewhere (tiled select) it stores them
+        from attention_lab import _native as nat
+        self.lists_only = nat.lib().attnlab_list_bytes(B, G, self.lo, self.hi, self.k, nat.ORDER_POSITION) > 0
 
     # -- algorithmic bytes per launch (per layer) --
+    def score_write_bytes(self):
+        """Per (b, g): the fp32 scores (only where the step stores them) and the bf16 z column."""
+        return (0 if self.lists_only else 4 * self.M) + 2 * self.r
+
     def score_bytes(self):
-        """The score kernel: index-table columns [lo, hi) read and fp32 scores written per (b, g), plus q_cat, k_new and
-        the z column written per (b, g) and the projection weights per group."""
+        """The score kernel: index-table columns [lo, hi) read per (b, g), the fp32 scores written where the step stores
+        them (not with the list select, whose step never puts its scores in HBM), q_cat, k_new and the z column per
+        (b, g), and the projection weights per group."""
         B, G, h, d, r, M = self.B, self.G, self.h, self.d, self.r, self.M
-        return B * G * (r * M * 2 + 4 * M + r * 2 + (h * d + d) * 2) + G * (h * d * r + r * d) * 2
+        return B * G * (r * M * 2 + self.score_write_bytes() + (h * d + d) * 2) + G * (h * d * r + r * d) * 2
 
     def select_bytes(self):
-        return self.B * self.G * (4 * self.M + 4 * self.k)
+        """Per (b, g): the k picks written, plus the scores read where the step stores them."""
+        return self.B * self.G * ((0 if self.lists_only else 4 * self.M) + 4 * self.k)
 
     def attend_bytes(self):
         B, G, h, d, S = self.B, self.G, self.h, self.d, self.S
@@ -326,21 +337,21 @@ def launchers(ls, torch):
                  h, ls.L, C, Pd, scale, ls.dense_out[l].data_ptr(), 1, part.data_ptr(), stream())
 
     def score(l):   # u, z column, scan (and the key lists) in one launch, as in the fused step: the dominant kernel
-        if list_bytes > 0:
+        if list_bytes > 0:   # key lists only, no score stored (the step's position order)
             nat.call("attnlab_score_grouped_lists", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
-                     ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), u_buf.data_ptr(), ls.scores.data_ptr(),
-                     ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, ls.k, nat.ORDER_POSITION,
-                     hist.data_ptr(), lists.data_ptr(), list_bytes, stream())
+                     ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), u_buf.data_ptr(), None, ls.scores.shape[2], B, G,
+                     r, C, d, h * d, ls.lo, ls.hi, ls.write_col, ls.k, nat.ORDER_POSITION, hist.data_ptr(),
+                     lists.data_ptr(), list_bytes, stream())
             return
         nat.call("attnlab_score_grouped", ls.zT[l].data_ptr(), ls.k_new[l].data_ptr(), ls.wk[l].data_ptr(),
                  ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), None, u_buf.data_ptr(), ls.scores.data_ptr(),
                  ls.scores.shape[2], B, G, r, C, d, h * d, ls.lo, ls.hi, ls.write_col, 1, hist.data_ptr(), stream())
 
     def select(l):
-        if list_bytes > 0:
-            nat.call("attnlab_select_lists", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k,
-                     C, nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), lists.data_ptr(),
-                     list_bytes, stream())
+        if list_bytes > 0:   # from the lists; a tile whose list is incomplete is recomputed from the table and u
+            nat.call("attnlab_select_lists", None, ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
+                     nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), lists.data_ptr(),
+                     list_bytes, ls.zT[l].data_ptr(), nat.DT_BF16, u_buf.data_ptr(), stream())
             return
         nat.call("attnlab_select_rows", ls.scores.data_ptr(), ls.scores.shape[2], B, G, ls.lo, ls.hi, ls.L, ls.k, C,
                  nat.ORDER_POSITION, ls.rows.data_ptr(), ls.S, None, hist.data_ptr(), sel_scratch.data_ptr(),

@@ -198,10 +198,14 @@ int attnlab_select_rows(const float* scores, int64_t score_stride, int B, int G,
  * reference's step is indexer + torch.topk, decode.py:86-93 and :145-163). attnlab_score_grouped_lists is the
  * one-launch attnlab_score_grouped (bf16 table, r = 32, h*d <= 512, C % 8 == 0, 16-byte aligned zT, u built from q_cat
  * and wq_t) that also writes, for every score workgroup, a list of its largest keys into `lists` (256-byte aligned,
- * attnlab_list_bytes(B, G, lo, hi, k) bytes, no initialisation); `state` is required. attnlab_select_lists then
- * writes what attnlab_select_rows writes for the same scores, state and arguments, reading the lists instead of every
- * score (a tile whose list cannot hold its part of the selection is read from the scores), in one launch, and leaves
- * the state zeroed. attnlab_list_bytes returns 0 where the list select does not apply (hi - lo > 32768, or k large
+ * attnlab_list_bytes(B, G, lo, hi, k, order) bytes, no initialisation); `state` is required; `out` may be NULL (key
+ * lists only, no score stored: what the fused step runs in position order), and then u_out must be given.
+ * attnlab_select_lists then writes what attnlab_select_rows writes for the same scores, state and arguments, reading
+ * the lists instead of every score, in one launch, and leaves the state zeroed. A tile whose list cannot hold its part
+ * of the selection (and a row whose threshold bin holds more than 8192 keys) is read from `scores`; with scores NULL
+ * it is recomputed from the index table zT (z_dtype ATTNLAB_DT_BF16 or ATTNLAB_DT_F32, the score stage's table) and
+ * the score stage's u_out, in the score kernel's exact fp32 operation order, so the result is the same; that takes
+ * ATTNLAB_ORDER_POSITION (score order reads the picks' scores back). zT and u are ignored when scores are given. attnlab_list_bytes returns 0 where the list select does not apply (hi - lo > 32768, or k large
  * against hi - lo, or `order` ATTNLAB_ORDER_SCORE with k > ATTNLAB_LDS_SORT_K, which the list select does not sort;
  * both functions then fail with ATTNLAB_EINVAL before any launch) and -1 for invalid sizes. `order` is the row order
  * the select stage will be asked for: the score stage refuses a combination the select stage would refuse, because
@@ -217,7 +221,8 @@ int attnlab_score_grouped_lists(uint16_t* zT, const uint16_t* k_new, const uint1
                                 uint32_t* state, void* lists, int64_t lists_bytes, void* stream);
 int attnlab_select_lists(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k,
                          int C, int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
-                         const void* lists, int64_t lists_bytes, void* stream);
+                         const void* lists, int64_t lists_bytes, const void* zT, int z_dtype, const float* u,
+                         void* stream);
 
 /* Scratch bytes of attnlab_select_rows / attnlab_topk_tiled for R rows of M candidates and top-k in `order`: the
  * tiled select's bitmaps and candidate entries, plus the radix pass's buffers in score order with

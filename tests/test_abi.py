@@ -148,8 +148,14 @@ def test_list_select_refuses_shapes_it_does_not_cover(native_lib):
                      9830, 1, 16, 256, 1 << 24, None)
     with pytest.raises(ValueError, match="does not apply"):   # M = 40000 > 32768
         _native.call("attnlab_select_lists", 16, 40000, 1, 8, 4, 40004, 40068, 100, 40100, 0, 16, 200, None, 16, 256,
-                     1 << 20, None)
+                     1 << 20, None, 0, None, None)
     with pytest.raises(ValueError, match="attnlab_list_bytes"):   # lists too small
         _native.call("attnlab_select_lists", 16, 2000, 1, 8, 4, 2004, 2068, 64, 2100, 0, 16, 200, None, 16, 256, 64,
-                     None)
+                     None, 0, None, None)
+    with pytest.raises(ValueError, match="without stored scores"):   # no scores: the table and u, position order
+        _native.call("attnlab_select_lists", None, 2000, 1, 8, 4, 2004, 2068, 64, 2104, 1, 16, 200, None, 16, 256,
+                     1 << 20, 16, 0, 16, None)
+    with pytest.raises(ValueError, match="without stored scores"):
+        _native.call("attnlab_select_lists", None, 2000, 1, 8, 4, 2004, 2068, 64, 2104, 0, 16, 200, None, 16, 256,
+                     1 << 20, None, 0, 16, None)
     assert native_lib.attnlab_sparse_decode_workspace(0, 8, 2, 4, 100, 164, 3, 1) == -1

@@ -23,29 +23,37 @@ def test_more_than_one_gpu_exits_with_a_message():
     assert line["n_gpus"] == 2 and "one GPU" in line["error"]
 
 
-def layer_stack(B, G, h, L, rho_k):
-    """A LayerStack's shape attributes without its tensors (the byte counts are arithmetic on them)."""
+def layer_stack(B, G, h, L, rho_k, lists_only=True):
+    """A LayerStack's shape attributes without its tensors (the byte counts are arithmetic on them). lists_only: the
+    step's list select, where the score kernel stores no score."""
     ls = bench.LayerStack.__new__(bench.LayerStack)
     ls.B, ls.G, ls.h, ls.d, ls.r, ls.L, ls.C = B, G, h, 128, 32, L, L
     ls.lo, ls.hi = 4, L - 64
     ls.M = ls.hi - ls.lo
     ls.k = rho_k
     ls.S = 68 + rho_k
+    ls.lists_only = lists_only
     return ls
 
 
 def test_algorithmic_bytes_follow_the_per_unit_formulas():
     """32K, rho = 1/32 (k = 1024, S = 1092), B = 1, G = 8, h = 2: the per-(b, g) figures of the measurement plan
     (zT columns + fp32 scores; scores + indices; K/V rows + row ids + q + bf16 out; the whole dense read)."""
-    ls = layer_stack(1, 8, 2, 32768, 1024)
+    ls = layer_stack(1, 8, 2, 32768, 1024, lists_only=False)
     M = 32700
     assert ls.score_bytes() == 8 * (32 * M * 2 + 4 * M + 32 * 2 + (2 * 128 + 128) * 2) + 8 * (2 * 128 * 32 + 32 * 128) * 2
     assert 8 * (32 * M * 2 + 4 * M) == 17_788_800        # the zT read + score write part: 17.79 MB
     assert ls.select_bytes() == 8 * (4 * M + 4 * 1024)
     assert ls.attend_bytes() == 8 * (1092 * 512 + 4 * 1092 + 2 * 128 * 2 * 2)
     assert ls.dense_bytes() == 8 * (32768 * 512 + 2 * 128 * 2 * 2)
+    big = layer_stack(16, 8, 4, 32768, 1024, lists_only=False)
+    assert big.score_bytes() + big.select_bytes() + big.attend_bytes() == 374_773_760   # stored scores, bench shape
+    # the list select's step: no score reaches HBM, so neither the score write nor the select's read is credited
+    ls = layer_stack(1, 8, 2, 32768, 1024)
+    assert ls.score_bytes() == 8 * (32 * M * 2 + 32 * 2 + (2 * 128 + 128) * 2) + 8 * (2 * 128 * 32 + 32 * 128) * 2
+    assert ls.select_bytes() == 8 * 4 * 1024
     big = layer_stack(16, 8, 4, 32768, 1024)
-    assert big.score_bytes() + big.select_bytes() + big.attend_bytes() == 374_773_760   # per layer at the bench shape
+    assert big.score_bytes() + big.select_bytes() + big.attend_bytes() == 374_773_760 - 128 * 8 * M
 
 
 def test_prefill_score_counts():

@@ -430,7 +430,7 @@ def test_list_select_stages_through_the_abi(gpu, B, h, C, L, rho):
                  idx.wq_t_scaled.data_ptr(), None, scores.data_ptr(), M, B, G, 32, C, 128, h * 128, lo, hi, L - 1, k,
                  order, state.data_ptr(), lists.data_ptr(), nbytes, stream)
         nat.call("attnlab_select_lists", scores.data_ptr(), M, B, G, lo, hi, L, k, C, order, rows.data_ptr(), S, None,
-                 state.data_ptr(), lists.data_ptr(), nbytes, stream)
+                 state.data_ptr(), lists.data_ptr(), nbytes, None, 0, None, stream)
         torch.cuda.synchronize()
         assert int(state.abs().sum()) == 0, "the list select left its state dirty"
         s = scores.view(B, G, M).cpu().numpy()
@@ -502,8 +502,47 @@ def test_list_stages_refuse_score_order_past_the_lds_sort(gpu):
     assert int(state.abs().sum()) == 0, "the refused score stage touched the state"
     score_stage(nat.ORDER_POSITION)
     nat.call("attnlab_select_lists", scores.data_ptr(), M, B, G, lo, hi, L, k, C, nat.ORDER_POSITION, rows.data_ptr(),
-             S, None, state.data_ptr(), lists.data_ptr(), nbytes, stream)
+             S, None, state.data_ptr(), lists.data_ptr(), nbytes, None, 0, None, stream)
     torch.cuda.synchronize()
     assert int(state.abs().sum()) == 0
     s = scores.view(B, G, M).cpu().numpy()
     assert np.array_equal(rows.view(B, G, S).cpu().numpy(), exact.select_rows(s, lo, hi, L, k, order="position"))
+
+
+@pytest.mark.parametrize("case", [None, "skewed_tile", "all_equal"])
+@pytest.mark.parametrize("B,h,C,L,rho", [(1, 2, 32768 + 64, 32768, 1 / 32), (16, 4, 16384, 16384, 1 / 32)])
+def test_list_stages_without_stored_scores(gpu, case, B, h, C, L, rho):
+    """The score stage writing key lists only (out NULL) and the list select recomputing what it needs from the table
+    and u (an incomplete list's tile, a row resolved by radix passes): rows bit-exact against the oracle on the scores
+    of the score kernel, equal to the same stages with stored scores, the state left zero."""
+    from attention_lab import _native as nat
+    G = 8
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=L + B + 3)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
+    if case:
+        _shape_scores(zT, lo, hi, case)
+    M = hi - lo
+    nbytes = nat.lib().attnlab_list_bytes(B, G, lo, hi, k, nat.ORDER_POSITION)
+    lists = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
+    u = torch.empty(B * G, 32, dtype=torch.float32, device=gpu)
+    qc = q_pre.reshape(B, G, h * 128).contiguous()
+    stream = nat.stream_of(gpu)
+    got = []
+    for stored in (False, True):
+        scores = torch.empty(B * G, M, dtype=torch.float32, device=gpu) if stored else None
+        rows = torch.empty(B * G, S, dtype=torch.int32, device=gpu)
+        nat.call("attnlab_score_grouped_lists", zT.data_ptr(), None, idx.wk.data_ptr(), qc.data_ptr(),
+                 idx.wq_t_scaled.data_ptr(), u.data_ptr(), nat.ptr(scores), M, B, G, 32, C, 128, h * 128, lo, hi, L - 1,
+                 k, nat.ORDER_POSITION, state.data_ptr(), lists.data_ptr(), nbytes, stream)
+        nat.call("attnlab_select_lists", nat.ptr(scores), M, B, G, lo, hi, L, k, C, nat.ORDER_POSITION,
+                 rows.data_ptr(), S, None, state.data_ptr(), lists.data_ptr(), nbytes, zT.data_ptr(), nat.DT_BF16,
+                 u.data_ptr(), stream)
+        torch.cuda.synchronize()
+        assert int(state.abs().sum()) == 0, f"stored={stored}: the list select left its state dirty"
+        got.append(rows.view(B, G, S).cpu().numpy())
+    s = kernel_scores(zT, q_pre, idx, lo, hi)
+    want = exact.select_rows(s, lo, hi, L, k, order="position")
+    assert np.array_equal(got[0], want), "recomputed scores: row list differs from the oracle"
+    assert np.array_equal(got[1], want)
