@@ -99,6 +99,10 @@ def parse_args():
                     help="instead of the bench line: the fused step over float32 index tables (a trained bank's "
                          "dtype) at the bench shape, 8 rotating layers, graph-timed, with the bf16 step beside it; "
                          "one JSON line (also the command profiled for the fp32 kernels)")
+    ap.add_argument("--gather-ceiling", action="store_true",
+                    help="instead of the bench line: the attend against a gather-only probe over the step's own row "
+                         "lists (every layer of a 36-layer stack, rows from the step itself), at B=16 h=4 and B=1 h=2, "
+                         "graph-timed per layer; one JSON line")
     ap.add_argument("--p-lengths", type=int, nargs="+", default=[8192, 16384, 32256], help="N0 of --p0 / --p1")
     ap.add_argument("--p-layers", type=int, default=28, help="rotating layers of --p0 / --p1")
     ap.add_argument("--prefill-workload", action="store_true",
@@ -1377,6 +1381,78 @@ def run_b1(torch, dev, args):
     return res
 
 
+def attend_head_groups(BG, h, P):
+    """The attend's head-group count for BG rows, h heads and P partitions (attend.hip head_groups)."""
+    Q = 1
+    while h % (2 * Q) == 0 and BG * Q * P < 256:
+        Q *= 2
+    return Q
+
+
+def gather_ceiling(torch, dev, args):
+    """The attend against the gather-only probe (attnlab_gather_probe: the same rows, grid, lanes and load pipeline,
+    no arithmetic) over the row lists the fused step itself selects, one list per layer of the stack, so every layer
+    reads other rows of another cache (nothing is served from the Infinity Cache across layers). Both in graphs of one
+    launch per layer, both layer orders, conservative medians per layer. The probe also runs at other splits of the same
+    rows: Q = 1 with P = 2 (each row loaded once, split over two workgroups) against the attend's Q = 2, P = 1 (each
+    row loaded by two head-group workgroups, the second read from L2)."""
+    from attention_lab import _native as nat
+    from attention_lab import hip_attend
+    out = {"probe": "attnlab_gather_probe: the attend's rows, grid, lane layout and 4-stage load pipeline; XOR-fold "
+                    "of the loaded words, one word stored per thread"}
+    for B, h in ((16, 4), (1, 2)):
+        ls = LayerStack(torch, dev, batch=B, groups=args.groups, hpg=h, context=args.context, layers=args.layers,
+                        r=args.index_dim, rho=args.rho, seed=args.seed)
+        G, d, C, S = ls.G, ls.d, ls.C, ls.S
+        lib = nat.lib()
+        P = hip_attend.sparse_partitions(B * G, S, h)
+        Q = attend_head_groups(B * G, h, P)
+        rows = [torch.empty(B * G, S, dtype=torch.int32, device=dev) for _ in range(ls.n)]
+        state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
+        wsb = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        part = torch.empty(B * G * max(P, 2) * h * 130, dtype=torch.float32, device=dev)
+        sink = torch.empty(B * G * 8 * 8 * 256, dtype=torch.int32, device=dev)
+        scale = 1.0 / math.sqrt(d)
+
+        def stream():
+            return torch.cuda.current_stream(dev).cuda_stream
+
+        for l in range(ls.n):   # the step's own selection of every layer, in position order
+            nat.call("attnlab_sparse_decode_step", ls.q[l].data_ptr(), ls.q_cat[l].data_ptr(), ls.K[l].data_ptr(),
+                     ls.V[l].data_ptr(), ls.zT[l].data_ptr(), ls.wq_t[l].data_ptr(), ls.wk[l].data_ptr(),
+                     ls.k_new[l].data_ptr(), B, G, h, ls.r, C, ls.lo, ls.hi, ls.L, ls.k, ls.write_col, scale,
+                     nat.ORDER_POSITION, P, state.data_ptr(), ws.data_ptr(), wsb, rows[l].data_ptr(), None,
+                     ls.out[l].data_ptr(), stream())
+        torch.cuda.synchronize()
+
+        def attend(l):
+            nat.call("attnlab_attend", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(),
+                     rows[l].data_ptr(), S, B, G, h, S, C, P, scale, ls.out[l].data_ptr(), 1, part.data_ptr(),
+                     stream())
+
+        def probe(q, p):
+            def fn(l):
+                nat.call("attnlab_gather_probe", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, rows[l].data_ptr(),
+                         S, B, G, S, C, q, p, sink.data_ptr(), stream())
+            return fn
+
+        unique = B * G * S * d * 2 * 2   # every listed K and V row once
+        res = {"attend": ordered_stats(torch, attend, ls.n, args.kernel_reps, 3, per=ls.n)["conservative_us"]}
+        splits = [(Q, P), (1, P * Q)] if Q > 1 else [(Q, P)]
+        for q, p in splits:
+            res[f"probe_Q{q}_P{p}"] = ordered_stats(torch, probe(q, p), ls.n, args.kernel_reps, 3,
+                                                    per=ls.n)["conservative_us"]
+        out[f"B{B}_h{h}"] = {"attend_Q_P": [Q, P], "rows_per_bg": S, "unique_row_bytes": unique,
+                             "us_per_layer": {k: round(v, 3) for k, v in res.items()},
+                             "unique_gbs": {k: round(unique / (v * 1e-6) / 1e9, 1) for k, v in res.items()}}
+        print(f"[gather] B={B} h={h}: {out[f'B{B}_h{h}']}", file=sys.stderr, flush=True)
+        del ls, rows, ws, part
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.pmc_summary:
@@ -1410,6 +1486,8 @@ def main() -> int:
         return run_c4(torch, dev, args)
     if args.c5:
         return run_c5(torch, dev, args)
+    if args.gather_ceiling:
+        return gather_ceiling(torch, dev, args)
     if args.f32_workload:
         return run_f32_workload(torch, dev, args)
     if args.p0:

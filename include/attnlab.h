@@ -336,6 +336,16 @@ int attnlab_sparse_decode_step_noalloc(const uint16_t* q_main, const uint16_t* q
                                        int legal, int k, int write_col, float scale, int order, int P,
                                        int32_t* rows_out, int64_t* rows_flat, uint16_t* out, void* stream);
 
+/*
+ * Measurement only (no reference counterpart): the read ceiling of attnlab_attend. Reads the K/V rows attnlab_attend
+ * would read for these rows, with its grid (B*G*Q*P workgroups of 256 threads: Q head groups, P partitions), lane
+ * layout and load pipeline, and folds the loaded words into one word per thread, stored to sink [B*G*Q*P*256] uint32.
+ * Nothing else is computed. Positions outside [0, C) read row 0, as attnlab_attend masks them.
+ */
+int attnlab_gather_probe(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                         const int32_t* rows, int64_t rows_stride, int B, int G, int S, int C, int Q, int P,
+                         uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
