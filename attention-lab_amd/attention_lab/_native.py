@@ -17,8 +17,9 @@ LIB_NAME = "libattnlab.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 8
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
-# score key), then 64 super-bin counts of 32 bins each (ATTNLAB_SELECT_STATE_WORDS)
-SELECT_STATE_WORDS = 2112
+# score key), 64 super-bin counts of 32 bins each, then 64 arrival counters of the step's attend partitions
+# (ATTNLAB_SELECT_STATE_WORDS)
+SELECT_STATE_WORDS = 2176
 
 ATTNLAB_OK, ATTNLAB_EINVAL, ATTNLAB_ERUNTIME = 0, 1, 2
 LDS_SORT_K = 8192   # ATTNLAB_LDS_SORT_K: score order past this k goes through the select scratch

@@ -18,6 +18,7 @@
 // second small kernel merges them; the kernel boundary is what makes the partials of other XCDs' L2s visible, which
 // is far cheaper on this part than a device-scope fence per block.
 #include "common.h"
+#include "select.h"
 
 namespace attnlab {
 
@@ -50,6 +51,11 @@ struct AttendArgs {
     const int32_t* block_table = nullptr;
     int64_t bt_stride = 0;
     int G = 1, page_shift = 0, num_pages = 0;
+    // in-kernel split-K merge (P > 1): arrival counters, one per (b, g, head group) at arrive[bg * arrive_stride + qg],
+    // zero on entry and left zero; the partition workgroup that arrives last merges the P partials. Null: the combine
+    // kernel merges them.
+    uint32_t* arrive = nullptr;
+    int64_t arrive_stride = 0;
 };
 
 __device__ __forceinline__ void merge_state(float& m, float& l, float& m2, float& l2, float& w1, float& w2) {
@@ -58,6 +64,15 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float& m2, float
     w2 = (m2 == -INFINITY) ? 0.0f : fast_exp2(m2 - mn);
     l = w1 * l + w2 * l2;
     m = mn;
+}
+
+// A partial's words for the in-kernel merge, written and read at system scope (past the L2 of the writing XCD).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_SYSTEM));
 }
 
 __device__ __forceinline__ void store_out(const AttendArgs& a, size_t idx, float v) {
@@ -270,7 +285,14 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
         }
     }
     __syncthreads();
-    for (int idx = tid; idx < hq * kHeadDim; idx += kAttThreads) {
+    // this thread's (head, dim) items: idx = tid + kAttThreads * t (hq * 128 <= 1024 items)
+    constexpr int kItems = (H * kHeadDim + kAttThreads - 1) / kAttThreads;
+    float own_m[kItems], own_l[kItems], own_a[kItems];
+    const bool merge_here = a.P > 1 && a.arrive != nullptr;
+#pragma unroll
+    for (int t = 0; t < kItems; ++t) {
+        const int idx = tid + kAttThreads * t;
+        if (idx >= hq * kHeadDim) break;
         const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
         float ms = -INFINITY;
 #pragma unroll
@@ -283,17 +305,84 @@ __global__ __launch_bounds__(kAttThreads) void attend_kernel(AttendArgs a) {
             ls += ww * red_ml[w][i][1];
             as += ww * red_acc[w][i][dim];
         }
+        own_m[t] = ms;
+        own_l[t] = ls;
+        own_a[t] = as;
         if (a.P == 1) {
             store_out(a, ((size_t)bg * h + h0 + i) * kHeadDim + dim, as / ls);
         } else {
             float* pp = a.part + (((size_t)bg * a.P + p) * h + h0 + i) * (kHeadDim + 2);
-            if (dim == 0) {
-                pp[0] = ms;
-                pp[1] = ls;
+            if (merge_here) {
+                // system scope: written through to memory, so the merging workgroup reads them on any XCD
+                if (dim == 0) {
+                    store_coherent(pp, ms);
+                    store_coherent(pp + 1, ls);
+                }
+                store_coherent(pp + 2 + dim, as);
+            } else {
+                if (dim == 0) {
+                    pp[0] = ms;
+                    pp[1] = ls;
+                }
+                pp[2 + dim] = as;
             }
-            pp[2 + dim] = as;
         }
     }
+    if (!merge_here) return;
+    // Arrival: every partial store of this workgroup has completed before its counter increment (the wait and the
+    // barrier); the workgroup that sees P - 1 earlier arrivals therefore finds every other partial in memory.
+    __shared__ uint32_t last_sh;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t* counter = a.arrive + (size_t)bg * a.arrive_stride + qg;
+    if (tid == 0)
+        last_sh = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.P - 1);
+    __syncthreads();
+    if (!last_sh) return;
+    // The last arrival merges the P partials of its heads in partition order, eight at a time with an online rescale:
+    // the arithmetic of attend_combine, so the output is the same bit for bit. Its own partial comes from registers.
+#pragma unroll
+    for (int t = 0; t < kItems; ++t) {
+        const int idx = tid + kAttThreads * t;
+        if (idx >= hq * kHeadDim) break;
+        const int i = idx / kHeadDim, dim = idx - i * kHeadDim;
+        const float* pb = a.part + ((size_t)bg * a.P * h + h0 + i) * (kHeadDim + 2);
+        float ms = -INFINITY, ls = 0.0f, as = 0.0f;
+        for (int q0 = 0; q0 < a.P; q0 += 8) {
+            float mv[8], lv[8], av[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                mv[u] = -INFINITY;
+                lv[u] = av[u] = 0.0f;
+                const int pq = q0 + u;
+                if (pq == p) {
+                    mv[u] = own_m[t];
+                    lv[u] = own_l[t];
+                    av[u] = own_a[t];
+                } else if (pq < a.P) {
+                    const float* pp = pb + (size_t)pq * h * (kHeadDim + 2);
+                    mv[u] = load_coherent(pp);
+                    lv[u] = load_coherent(pp + 1);
+                    av[u] = load_coherent(pp + 2 + dim);
+                }
+            }
+            float mn = ms;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) mn = fmaxf(mn, mv[u]);
+            const float w0 = (ms == -INFINITY) ? 0.0f : fast_exp2(ms - mn);
+            ls *= w0;
+            as *= w0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float w = (mv[u] == -INFINITY) ? 0.0f : fast_exp2(mv[u] - mn);
+                ls += w * lv[u];
+                as += w * av[u];
+            }
+            ms = mn;
+        }
+        store_out(a, ((size_t)bg * h + h0 + i) * kHeadDim + dim, as / ls);
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // leave it zero
 }
 
 // Merge the P partials of every (b, g): thread -> (head, dim). Partials are read eight at a time, all loads of a group
@@ -355,7 +444,7 @@ static int launch_attend(const AttendArgs& a, int BG, hipStream_t s) {
     else if (hq <= 2) hipLaunchKernelGGL((attend_kernel<2, kStages, DENSE, PAGED>), grid, block, 0, s, a);
     else if (hq <= 4) hipLaunchKernelGGL((attend_kernel<4, kStages, DENSE, PAGED>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attend_kernel<8, kStages, DENSE, PAGED>), grid, block, 0, s, a);
-    if (a.P > 1) hipLaunchKernelGGL(attend_combine, dim3(BG), dim3(a.h * kHeadDim), 0, s, a);
+    if (a.P > 1 && a.arrive == nullptr) hipLaunchKernelGGL(attend_combine, dim3(BG), dim3(a.h * kHeadDim), 0, s, a);
     return check_launch(PAGED ? "attend_paged" : (DENSE ? "dense_decode" : "attend"));
 }
 
@@ -379,16 +468,30 @@ static int check_common(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stri
 
 using namespace attnlab;
 
-extern "C" int attnlab_attend(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
-                              const uint16_t* q, const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S,
-                              int C, int P, float scale, void* out, int out_bf16, float* part, void* stream) {
+int attnlab::attend_impl(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                         const uint16_t* q, const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int C,
+                         int P, float scale, void* out, int out_bf16, float* part, uint32_t* arrive,
+                         int64_t arrive_stride, hipStream_t stream) {
     const int rc = check_common(K, V, kv_bg_stride, kv_row_stride, q, B, G, h, C, P, out, part);
     if (rc) return rc;
     ATTNLAB_REQUIRE(S >= 1, "at least one row must be selected (S=%d)", S);
     ATTNLAB_REQUIRE(rows != nullptr && rows_stride >= S, "rows must hold S=%d positions per (b, g)", S);
     AttendArgs a{K, V, kv_bg_stride, kv_row_stride, q, rows, rows_stride, S, C, h, P, head_groups(B * G, h, P),
                  scale * kLog2e, out, out_bf16, part};
-    return launch_attend<false>(a, B * G, reinterpret_cast<hipStream_t>(stream));
+    if (P > 1 && arrive != nullptr) {
+        ATTNLAB_REQUIRE(a.Q <= kArriveWords && arrive_stride >= a.Q, "arrival counters too small for %d head groups",
+                        a.Q);
+        a.arrive = arrive;
+        a.arrive_stride = arrive_stride;
+    }
+    return launch_attend<false>(a, B * G, stream);
+}
+
+extern "C" int attnlab_attend(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                              const uint16_t* q, const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S,
+                              int C, int P, float scale, void* out, int out_bf16, float* part, void* stream) {
+    return attend_impl(K, V, kv_bg_stride, kv_row_stride, q, rows, rows_stride, B, G, h, S, C, P, scale, out, out_bf16,
+                       part, nullptr, 0, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int attnlab_dense_decode(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,

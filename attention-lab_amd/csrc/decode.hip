@@ -115,7 +115,10 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
         rc = select_rows_impl(scores, L.score_stride, B, G, lo, hi, legal, k, C, order, rows, S, rows_flat, state,
                               k > 0 ? ws + L.sel : nullptr, L.part - L.sel, s);
     if (rc) return rc;
-    return attnlab_attend(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part, stream);
+    // with the select state (k > 0) the attend merges its split-K partials itself, counting arrivals in the state's
+    // counter words (the select has just zeroed them); without it the combine kernel merges them
+    return attend_impl(K, V, (int64_t)C * d, d, q_main, rows, S, B, G, h, S, C, P, scale, out, 1, part,
+                       state ? state + kArriveOffset : nullptr, kSelectStateWords, s);
 }
 
 }  // namespace

@@ -11,12 +11,16 @@ namespace attnlab {
 constexpr int kHistBits = 11;                 // first digit: sign, exponent and the top two mantissa bits
 constexpr int kHistBins = 1 << kHistBits;
 constexpr int kHistShift = 32 - kHistBits;
-// Per-row select state shared by the score and select kernels: the first-digit histogram (kHistBins words), then
-// kSuperBins counts of 32 consecutive bins each (so the threshold's first digit is found from 64 + 32 words instead of
-// 2048). Zero before the first call; the select leaves it zero.
+// Per-row select state shared by the score, select and attend kernels of the fused step: the first-digit histogram
+// (kHistBins words), then kSuperBins counts of 32 consecutive bins each (so the threshold's first digit is found from
+// 64 + 32 words instead of 2048), then kArriveWords arrival counters of the attend's partitions (one per head group,
+// the in-kernel split-K merge). Zero before the first call; the select leaves every word zero (after the score kernel
+// and before the attend), and the attend leaves its counters zero.
 constexpr int kSuperBins = kHistBins / 32;
-constexpr int kSelectStateWords = kHistBins + kSuperBins;
-static_assert(kSelectStateWords == 2112, "ABI: ATTNLAB_SELECT_STATE_WORDS");
+constexpr int kArriveOffset = kHistBins + kSuperBins;
+constexpr int kArriveWords = 64;
+constexpr int kSelectStateWords = kArriveOffset + kArriveWords;
+static_assert(kSelectStateWords == ATTNLAB_SELECT_STATE_WORDS, "ABI: ATTNLAB_SELECT_STATE_WORDS");
 
 // Score order sorts up to this many selected pairs in LDS (64 KB); past it the select stages the picks in position
 // order and a radix pass over a scratch buffer lists them by score (only the tiled and single-workgroup selects).
@@ -313,6 +317,13 @@ inline ScoreLists list_layout(void* base, int R, FusedGeometry g, ListPlan p) {
 int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,
                       int order, int32_t* rows, int64_t rows_stride, int64_t* rows_flat, uint32_t* state,
                       const ScoreLists& lists, FusedGeometry geo, hipStream_t stream, TableRef table = TableRef{});
+
+// attnlab_attend with, when `arrive` is given and P > 1, the split-K merge inside the attend kernel instead of the
+// combine kernel: per (b, g) row one arrival counter per head group at arrive + bg * arrive_stride, zero on entry and
+// left zero (the fused step's select state holds them).
+int attend_impl(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride, const uint16_t* q,
+                const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int C, int P, float scale,
+                void* out, int out_bf16, float* part, uint32_t* arrive, int64_t arrive_stride, hipStream_t stream);
 
 // attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,

@@ -45,8 +45,9 @@ extern "C" {
 #define ATTNLAB_DT_F32 2
 
 /* Words per row of the select state shared by attnlab_score_grouped and attnlab_select_rows: the first-digit
- * histogram (2048 bins), then 64 super-bin counts (sums of 32 consecutive bins). */
-#define ATTNLAB_SELECT_STATE_WORDS 2112
+ * histogram (2048 bins), then 64 super-bin counts (sums of 32 consecutive bins), then 64 arrival counters that the
+ * fused step's attend uses to merge its split-K partials in-kernel. Zero on entry; every call leaves it zero. */
+#define ATTNLAB_SELECT_STATE_WORDS 2176
 
 /* ABI version; bumped on any signature change. */
 int attnlab_abi_version(void);

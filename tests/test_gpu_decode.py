@@ -546,3 +546,30 @@ def test_list_stages_without_stored_scores(gpu, case, B, h, C, L, rho):
     want = exact.select_rows(s, lo, hi, L, k, order="position")
     assert np.array_equal(got[0], want), "recomputed scores: row list differs from the oracle"
     assert np.array_equal(got[1], want)
+
+
+@pytest.mark.parametrize("G,h,P", [(3, 2, 3), (3, 2, 8), (8, 2, 5), (8, 4, 16), (1, 2, 8)])
+def test_in_kernel_partition_merge_equals_the_combine_kernel(gpu, G, h, P):
+    """The step merges its split-K partials inside the attend kernel (the last partition workgroup to arrive, counted
+    in the select state). Grids of 3 x 2 x 3 or 3 x 2 x 8 workgroups put a (b, g)'s partitions on several XCDs. Two
+    calls with different queries: each output equals, bit for bit, attnlab_attend with the combine kernel over the
+    same rows and partitions, and meets the bf16 bar against the float64 oracle; the state is left zero."""
+    from attention_lab import _native as nat
+    B, C, L = 1, 8192 + 64, 8192
+    ws = nat.Workspace()
+    for call in range(2):
+        K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, G=G, h=h, C=C, seed=100 + 10 * G + call)
+        req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=1 / 8, device=gpu)
+        out, flat = sparse_decode_step_kernel(q, q_pre, K, V, zT, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo,
+                                              req.layout.candidate_lo, req.layout.candidate_hi, req.k,
+                                              req.selected_count, k_pre_new=k_pre_new, write_col=req.write_col,
+                                              return_rows=True, canonical_order=True, partitions=P, workspace=ws)
+        torch.cuda.synchronize()
+        S = req.selected_count
+        pos = (flat.view(B, G, S) - req.offsets).to(torch.int32).contiguous()
+        ref = hip_attend.attend(q.reshape(B, G, h, 128).contiguous(), K, V, pos, partitions=P)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(B, G, h, 128), ref), f"call {call}: in-kernel merge differs from the combine kernel"
+        want = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), pos.cpu().numpy())
+        check_out(out, want, f"G={G} P={P} call {call}")
+        assert int(ws.bytes(gpu, 0, "state").abs().sum()) == 0, "arrival counters left non-zero"
