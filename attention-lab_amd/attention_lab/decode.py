@@ -269,7 +269,7 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
             raise ValueError(f"write_col={write_col} must lie in [0, C) and outside [lo, hi)")
     else:
         wc = 0
-    P = hip_attend.sparse_partitions(B * G, S, h) if partitions is None else int(partitions)
+    P = hip_attend.sparse_partitions(B * G, S, h, merged=k > 0) if partitions is None else int(partitions)
     sc = float(1.0 / math.sqrt(d) if scale is None else scale)
     order = nat.ORDER_POSITION if canonical_order else nat.ORDER_SCORE
     nbytes = nat.lib().attnlab_sparse_decode_workspace(B, G, h, lo, hi, legal, k, P)

@@ -180,16 +180,36 @@ def auto_partitions(BG: int, rows: int, *, max_p: int, min_rows: int, blocks: in
     return max(1, min(max_p, want, cap))
 
 
-def sparse_partitions(BG: int, rows: int, h: int = 1) -> int:
-    """Split-K count of the sparse read. The kernel also splits each (b, g) over up to h head groups (powers of two
+def sparse_partitions(BG: int, rows: int, h: int = 1, merged: bool = False) -> int:
+    """Split-K count of the sparse read. `merged`: for the fused decode step, whose attend merges its partials in-kernel
+    (no combine launch) - see merged_partitions. Otherwise (the standalone attend, merged by the combine kernel): The kernel also splits each (b, g) over up to h head groups (powers of two
     dividing h) until the grid reaches one workgroup per CU; those count towards the 256 workgroups. With four head
     groups and at least 32 (b, g) rows the target is 512: splitting the rows further beats splitting the heads there
     (MI355X, 32K, S = 1092, per layer: B=4, h=4 33.2 us at P=4 against 34.1 at P=2; B=8 48.8 at P=2 against 49.5 at
     P=1; with eight head groups, B=4, the 256 target is 0.2 us better). With one head per KV group and at least 128
     (b, g) rows it is 128 (B=16, h=1: 73.7 us at P=1 against 74.3 at P=2; B=8 keeps P=4, 45.6 us)."""
+    if merged:
+        return merged_partitions(BG, rows, h)
     hg = h & -h if h > 0 else 1   # largest power of two dividing h
     blocks = 512 if hg == 4 and BG >= 32 else 128 if hg == 1 and BG >= 128 else 256
     return auto_partitions(BG * hg, rows, max_p=MAX_P, min_rows=128, blocks=blocks)
+
+
+def merged_partitions(BG: int, rows: int, h: int = 1) -> int:
+    """Split-K count of the fused step's attend (partials merged in-kernel by the last partition to arrive). About 256
+    workgroups over the chip, split by rows first (each row read once) and by head groups after (the kernel adds head
+    groups, which read the same rows twice, until the grid reaches 256); at least 128 rows per partition, at most 16
+    partitions, or 8 with four or more heads per KV group, where two head groups also come first from 32 (b, g) rows
+    on (a four-head workgroup's arithmetic then costs more than the second read).
+    Measured on MI355X, step per layer, the rule's P against the best of P in {1, 2, 4, 8, 16, 32}:
+    32K (S = 1092): B=1..2 P=8 best for h = 1, 2, 4; B=4 h=1 P=8 (30.8 us), h=2 P=8 31.79 against P=4 31.45, h=4
+    P=4 (32.8); B=8 P=4 / 4 / 2 best for h = 1 / 2 / 4; B=16 P=2 / 2 / 1 best (h=1 70.39 against 72.14 at P=1).
+    128K (S = 4164): B=1 h=2 P=16 best (40.39), h=4 P=8 40.9 against P=16 40.69; B=2 h=2 P=16 54.57 against P=8
+    54.2, h=4 P=8 best (56.04; 59.58 at P=4); B=4 h=2 P=8 best (93.11), h=4 P=4 best (95.36)."""
+    hg = h & -h if h > 0 else 1
+    q = 2 if hg >= 4 and BG >= 32 else 1
+    max_p = 8 if hg >= 4 else 16
+    return auto_partitions(BG * q, rows, max_p=max_p, min_rows=128, blocks=256)
 
 
 def dense_partitions(BG: int, length: int) -> int:

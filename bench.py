@@ -310,11 +310,12 @@ def launchers(ls, torch):
     lib = nat.lib()
     dev = ls.K[0].device
     B, G, h, d, r, C = ls.B, ls.G, ls.h, ls.d, ls.r, ls.C
-    P = hip_attend.sparse_partitions(B * G, ls.S, h)
+    P = hip_attend.sparse_partitions(B * G, ls.S, h, merged=True)   # the step: partials merged in-kernel
+    Pa = hip_attend.sparse_partitions(B * G, ls.S, h)                # the standalone attend: the combine kernel
     Pd = hip_attend.dense_partitions(B * G, ls.L)
     ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, ls.lo, ls.hi, ls.L, ls.k, P)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    part = torch.empty(B * G * max(P, Pd) * h * 130, dtype=torch.float32, device=dev)
+    part = torch.empty(B * G * max(P, Pa, Pd) * h * 130, dtype=torch.float32, device=dev)
     # select state (top-k histograms and counters): zero once; each score/select pair leaves it zeroed
     step_hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
     hist = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
@@ -365,13 +366,14 @@ def launchers(ls, torch):
         score(l)
         select(l)
 
-    def attend(l):
+    def attend(l):   # the standalone attend (split-K partials merged by the combine kernel)
         nat.call("attnlab_attend", ls.K[l].data_ptr(), ls.V[l].data_ptr(), C * d, d, ls.q[l].data_ptr(),
-                 ls.rows.data_ptr(), ls.S, B, G, h, ls.S, C, P, scale, ls.out[l].data_ptr(), 1, part.data_ptr(),
+                 ls.rows.data_ptr(), ls.S, B, G, h, ls.S, C, Pa, scale, ls.out[l].data_ptr(), 1, part.data_ptr(),
                  stream())
 
     return {"sparse": sparse, "dense": dense, "score": score, "select": select, "attend": attend,
-            "score_select": score_select, "hist": hist, "partitions": P, "dense_partitions": Pd,
+            "score_select": score_select, "hist": hist, "partitions": P, "attend_partitions": Pa,
+            "dense_partitions": Pd,
             "select_kernels": "select_lists" if list_bytes > 0 else "select_classify_compact + select_resolve_compact",
             "_keep": (ws, part, step_hist, u_buf, sel_scratch, lists)}
 
@@ -380,21 +382,27 @@ def kernel_breakdown(torch, fns, ls, reps):
     """Per-layer us of each stage of the fused step, from graphs of one launch per layer on consistent data, each
     stage in forward and reverse layer order (median, p95, conservative): score (u, z column, scan and, where the list
     select applies, its key lists: one kernel), select = (score + select) - score (the select consumes and clears the
-    histogram the scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend (+ split-K
-    merge). The flat figures are the conservative medians; `mean` holds the forward-order means (the kernel-trace
-    averages compare with these)."""
+    histogram the scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend = step -
+    (score + select) (the step's attend merges its split-K partials in-kernel), and attend_standalone, attnlab_attend
+    with the combine kernel. The flat figures are the conservative medians; `mean` holds the forward-order means (the
+    kernel-trace averages compare with these)."""
     n = ls.n
     score = ordered_stats(torch, fns["score"], n, reps, 3, per=n)
     fns["hist"].zero_()
     torch.cuda.synchronize()
     pair = ordered_stats(torch, fns["score_select"], n, reps, 3, per=n)
-    attend = ordered_stats(torch, fns["attend"], n, reps, 3, per=n)
-    select = {o: {k: pair[o][k] - score[o][k] for k in ("median_us", "mean_us")} for o in ("forward", "reverse")}
-    select["conservative_us"] = max(select["forward"]["median_us"], select["reverse"]["median_us"])
+    step = ordered_stats(torch, fns["sparse"], n, reps, 3, per=n)
+    standalone = ordered_stats(torch, fns["attend"], n, reps, 3, per=n)
+    diff = lambda a, b: {o: {k: a[o][k] - b[o][k] for k in ("median_us", "mean_us")} for o in ("forward", "reverse")}
+    select, attend = diff(pair, score), diff(step, pair)
+    for x in (select, attend):
+        x["conservative_us"] = max(x["forward"]["median_us"], x["reverse"]["median_us"])
     return {"score": score["conservative_us"], "select": select["conservative_us"], "attend": attend["conservative_us"],
-            "mean": {"score": score["forward"]["mean_us"], "select": pair["forward"]["mean_us"] - score["forward"]["mean_us"],
+            "attend_standalone": standalone["conservative_us"],
+            "mean": {"score": score["forward"]["mean_us"], "select": select["forward"]["mean_us"],
                      "attend": attend["forward"]["mean_us"]},
-            "orders": {"score": score, "score_select": pair, "select": select, "attend": attend}}
+            "orders": {"score": score, "score_select": pair, "step": step, "select": select, "attend": attend,
+                       "attend_standalone": standalone}}
 
 
 def capture(torch, fn, layers, reverse=False):
@@ -902,7 +910,7 @@ def run_f32_workload(torch, dev, args, layers=8):
     lo, hi, k = lay.candidate_lo, lay.candidate_hi, lay.clamp_k(fixed_budget(L, args.rho))
     S, C, M = lay.fixed_count + k, L, lay.candidate_count
     lib = nat.lib()
-    P = hip_attend.sparse_partitions(B * G, S, h)
+    P = hip_attend.sparse_partitions(B * G, S, h, merged=True)
     ws_bytes = lib.attnlab_sparse_decode_workspace(B, G, h, lo, hi, L, k, P)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=dev)
@@ -1372,7 +1380,7 @@ def run_b1(torch, dev, args):
         us = sp["conservative_us"]
         res[f"h{hpg}"] = {"sparse_us_per_layer": us, "dense_us_per_layer": dn["conservative_us"],
                           "sparse_orders": sp, "dense_orders": dn,
-                          "kernel_us": {k: per[k] for k in ("score", "select", "attend")},
+                          "kernel_us": {k: per[k] for k in ("score", "select", "attend", "attend_standalone")},
                           "sparse_algorithmic_bytes_per_layer": sparse_bytes,
                           "sparse_gbs": sparse_bytes / (us * 1e-6) / 1e9,
                           "sparse_frac_of_peak": sparse_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
@@ -1571,7 +1579,8 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": sb, "avg_launch_us": score_us},
         "timing": timing,
         "per_layer_us": {"sparse": us_layer, "sparse_conservative": us_layer_cons, "dense": ms_dense * 1e3 / ls.n,
-                         "score": kus["score"], "select": kus["select"], "attend_with_combine": kus["attend"],
+                         "score": kus["score"], "select": kus["select"], "attend": kus["attend"],
+                         "attend_standalone": kus["attend_standalone"],
                          "select_kernels": fns["select_kernels"],
                          "note": "sparse: the timed region's mean; the kernel figures and dense: conservative medians "
                                  "(slower of forward / reverse layer order); kernel_orders holds every order's median, "
