@@ -106,9 +106,10 @@ def test_mfma_busy_fraction(tmp_path, capsys):
 
 def test_committed_profiles_feed_the_bench_line():
     """The committed score-kernel PMC summary gives the bench line's traffic: at least the algorithmic bytes of one
-    B=16, 32K launch (285,120,512) and within a few percent of them (the histogram atomics and the key lists)."""
+    B=16, 32K launch as the step runs it (268,378,112: no score stored) and within a few percent of them (the histogram
+    atomics and the key lists)."""
     traffic = bench.measured_traffic()
-    assert traffic is not None and 285_120_512 <= traffic <= 1.05 * 285_120_512
+    assert traffic is not None and 268_378_112 <= traffic <= 1.05 * 268_378_112
     assert 0.0 < bench.mfma_busy_from_profile() < 1.0
 
 
