@@ -56,6 +56,7 @@ SIGNATURES = {
     "attnlab_sparse_decode_step_f32": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
     "attnlab_sparse_decode_step_noalloc": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _p, _p]),
     "attnlab_gather_probe": (_i, [_p, _p, _i64, _i, _p, _i64] + [_i] * 6 + [_p, _p]),
+    "attnlab_scan_probe": (_i, [_p, _p, _p] + [_i] * 6 + [_p, _p]),
 }
 
 _lock = threading.Lock()

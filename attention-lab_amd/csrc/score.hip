@@ -33,6 +33,7 @@ struct ScoreArgs {
     int tiles;              // column tiles per (b, g) row
     uint32_t* hist;         // [BG, kSelectStateWords] select state: first-digit histogram bins first, or null
     ScoreLists lists;       // per-workgroup key lists (entries null: none; score_scan_fused only)
+    uint32_t* sink = nullptr;   // score_scan_fused<NSUB, true> (the read probe): one folded word per thread
 };
 
 constexpr int kMaxR = 32;
@@ -292,7 +293,9 @@ __global__ __launch_bounds__(BLOCK) void score_scan_v16(ScoreArgs a) {
 // double-buffered (the loads of sub-tile s + 1 are issued before sub-tile s is reduced), which spreads the weight reads
 // and the histogram flush over NSUB sub-tiles.
 // The workgroup of tile 0 also writes the z column and, when asked, u.
-template <int NSUB>
+// PROBE (measurement only, attnlab_scan_probe): the same grid, prologue, loads and pipeline, but every loaded word is
+// XOR-folded instead of multiplied, and nothing is reduced, counted, listed or stored beyond one word per thread.
+template <int NSUB, bool PROBE = false>
 __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     constexpr int kCols = 512;
     constexpr int kUIter = 512 / 64;   // q_cat features per lane
@@ -369,6 +372,18 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     if (tid < 2) lcount[tid] = 0u;
     __syncthreads();
 
+    if constexpr (PROBE) {
+        uint32_t fx = __float_as_uint(u[0]) & 1u;
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if (s + kDepth - 1 < NSUB) load(s + kDepth - 1, vb[(s + kDepth - 1) % kDepth]);
+            const u32x4_t (&v)[8] = vb[s % kDepth];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) fx ^= v[jj].x ^ v[jj].y ^ v[jj].z ^ v[jj].w;
+        }
+        a.sink[(size_t)lin * 256 + tid] = fx;
+        return;
+    }
     // a.out null (key lists only, the fused step's position order): no score is stored; the list select recomputes
     // the few tiles it needs from the table
     float* o = a.out ? a.out + (size_t)bg * a.out_stride - lo : nullptr;
@@ -746,6 +761,26 @@ __global__ __launch_bounds__(256) void score_lightning(LightningArgs a) {
 }  // namespace attnlab
 
 using namespace attnlab;
+
+extern "C" int attnlab_scan_probe(const uint16_t* zT, const uint16_t* q_cat, const uint16_t* wq_t, int B, int G,
+                                  int C, int hd, int lo, int hi, uint32_t* sink, void* stream) {
+    ATTNLAB_REQUIRE(B >= 1 && G >= 1 && 0 <= lo && lo < hi && hi <= C && hd >= 1,
+                    "need B, G, hd >= 1 and 0 <= lo < hi <= C");
+    ATTNLAB_REQUIRE(zT && q_cat && wq_t && sink, "zT, q_cat, wq_t and sink must be device pointers");
+    const FusedGeometry geo = fused_geometry(B * G, C, 32, hd, lo, hi, zT, false);
+    ATTNLAB_REQUIRE(geo.nsub > 0 && reinterpret_cast<uintptr_t>(wq_t) % 16 == 0,
+                    "the probe needs the one-launch score's layout (C %% 8 == 0, 16-byte aligned zT and wq_t, h*d <= 512)");
+    ScoreArgs a{const_cast<uint16_t*>(zT), nullptr, nullptr, q_cat, wq_t, nullptr, nullptr, nullptr, 0, G, 32, C, 128, hd,
+                lo, hi - lo, 0, geo.tiles, nullptr, ScoreLists{nullptr, nullptr, 0, 0}};
+    a.sink = sink;
+    const dim3 grid(B * G * geo.tiles), block(256);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (geo.nsub == 8) hipLaunchKernelGGL((score_scan_fused<8, true>), grid, block, 0, s, a);
+    else if (geo.nsub == 4) hipLaunchKernelGGL((score_scan_fused<4, true>), grid, block, 0, s, a);
+    else if (geo.nsub == 2) hipLaunchKernelGGL((score_scan_fused<2, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((score_scan_fused<1, true>), grid, block, 0, s, a);
+    return check_launch("scan_probe");
+}
 
 extern "C" int attnlab_score_grouped(uint16_t* zT, const uint16_t* k_new, const uint16_t* wk, const uint16_t* q_cat,
                                      const uint16_t* wq_t, const float* u_in, float* u_out, float* out,

@@ -99,6 +99,8 @@ def parse_args():
                     help="instead of the bench line: the fused step over float32 index tables (a trained bank's "
                          "dtype) at the bench shape, 8 rotating layers, graph-timed, with the bf16 step beside it; "
                          "one JSON line (also the command profiled for the fp32 kernels)")
+    ap.add_argument("--scan-ceiling", action="store_true",
+                    help="instead of the bench line: the fused score kernel against its read probe (attnlab_scan_probe)")
     ap.add_argument("--gather-ceiling", action="store_true",
                     help="instead of the bench line: the attend against a gather-only probe over the step's own row "
                          "lists (every layer of a 36-layer stack, rows from the step itself), at B=16 h=4 and B=1 h=2, "
@@ -1461,6 +1463,38 @@ def gather_ceiling(torch, dev, args):
     return 0
 
 
+def scan_ceiling(torch, dev, args):
+    """The fused score kernel (the step's launch: u, z column, scan, histogram and key lists) against its read probe
+    (attnlab_scan_probe: the same grid, u prologue, table loads and load pipeline, with the multiply, reduction,
+    histogram and lists replaced by an XOR fold of the loaded words) over the same 36 layers' index tables, in graphs of
+    one launch per layer, both layer orders, conservative medians per layer."""
+    from attention_lab import _native as nat
+    out = {"probe": "attnlab_scan_probe: score_scan_fused's grid, u prologue, table loads and pipeline; XOR-fold of "
+                    "the loaded words, one word stored per thread"}
+    for B, h in ((16, 4), (1, 2)):
+        ls = LayerStack(torch, dev, batch=B, groups=args.groups, hpg=h, context=args.context, layers=args.layers,
+                        r=args.index_dim, rho=args.rho, seed=args.seed)
+        fns = launchers(ls, torch)
+        G, C = ls.G, ls.C
+        sink = torch.empty(B * G * ((ls.hi - ls.lo + 16 + 511) // 512) * 256, dtype=torch.int32, device=dev)
+
+        def probe(l):
+            nat.call("attnlab_scan_probe", ls.zT[l].data_ptr(), ls.q_cat[l].data_ptr(), ls.wq_t[l].data_ptr(), B, G, C,
+                     h * ls.d, ls.lo, ls.hi, sink.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+
+        table = B * G * ls.r * (ls.hi - ls.lo) * 2   # every candidate column of every index row, once
+        res = {"score": ordered_stats(torch, fns["score"], ls.n, args.kernel_reps, 3, per=ls.n)["conservative_us"],
+               "probe": ordered_stats(torch, probe, ls.n, args.kernel_reps, 3, per=ls.n)["conservative_us"]}
+        out[f"B{B}_h{h}"] = {"table_bytes": table, "us_per_layer": {k: round(v, 3) for k, v in res.items()},
+                             "table_gbs": {k: round(table / (v * 1e-6) / 1e9, 1) for k, v in res.items()},
+                             "score_over_probe": round(res["score"] / res["probe"], 4)}
+        print(f"[scan] B={B} h={h}: {out[f'B{B}_h{h}']}", file=sys.stderr, flush=True)
+        del ls, fns, sink
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.pmc_summary:
@@ -1496,6 +1530,8 @@ def main() -> int:
         return run_c5(torch, dev, args)
     if args.gather_ceiling:
         return gather_ceiling(torch, dev, args)
+    if args.scan_ceiling:
+        return scan_ceiling(torch, dev, args)
     if args.f32_workload:
         return run_f32_workload(torch, dev, args)
     if args.p0:

@@ -347,6 +347,17 @@ int attnlab_gather_probe(const uint16_t* K, const uint16_t* V, int64_t kv_bg_str
                          const int32_t* rows, int64_t rows_stride, int B, int G, int S, int C, int Q, int P,
                          uint32_t* sink, void* stream);
 
+/*
+ * Measurement only (no reference counterpart): the read ceiling of the one-launch score (score_scan_fused, the fused
+ * step's score). Runs its grid, u prologue (q_cat [B*G, hd] . wq_t [G, hd, 32]), table loads of zT [B*G, 32, C] over
+ * candidate columns [lo, hi) and load pipeline, with the multiply, reduction, histogram and key lists replaced by an
+ * XOR fold of the loaded words; one word per thread goes to sink, which must hold
+ * B*G*ceil((hi - lo + 16) / 512)*256 uint32. Needs the one-launch layout: C % 8 == 0, zT and wq_t 16-byte aligned,
+ * 1 <= hd <= 512.
+ */
+int attnlab_scan_probe(const uint16_t* zT, const uint16_t* q_cat, const uint16_t* wq_t, int B, int G, int C, int hd,
+                       int lo, int hi, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
