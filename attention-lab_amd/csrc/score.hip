@@ -332,9 +332,24 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     // step, 135 VGPRs and three waves per SIMD), one ahead otherwise (equal or 0.1 us better at 2 and 4)
     constexpr int kDepth = NSUB >= 8 ? 3 : 2;
     u32x4_t vb[kDepth][8];
+    // The z column (tile 0) in a grid of at most one workgroup per CU: its loads go out first and its dot products
+    // follow u, so that the tile-0 workgroups do not end a memory round trip after the others (B=1, 32K: score 7.45 ->
+    // 7.23 us). Larger grids keep it at the end (no gain there; at B=16 the early form cost 0.5 us), as do other
+    // layouts (write_z).
+    const uint16_t* kn = a.k_new ? a.k_new + (size_t)bg * a.d : nullptr;
+    const bool z_early = !PROBE && tile == 0 && gridDim.x <= 256 && kn != nullptr && a.d == 128 &&
+                         ((reinterpret_cast<uintptr_t>(a.wk) | reinterpret_cast<uintptr_t>(kn)) & 15) == 0;
     {
         const uint16_t* qp = a.q_cat + (size_t)bg * a.hd;
         const uint16_t* wp = a.wq_t + (size_t)g * a.hd * 32 + 8 * wave;
+        uint4 zw0, zw1, zk0, zk1;
+        if (z_early) {   // thread -> index row tid / 8, dims 16 (tid % 8) .. + 15, as write_z
+            const uint16_t* wr = a.wk + ((size_t)g * 32 + (tid >> 3)) * 128 + (tid & 7) * 16;
+            zw0 = *reinterpret_cast<const uint4*>(wr);
+            zw1 = *reinterpret_cast<const uint4*>(wr + 8);
+            zk0 = *reinterpret_cast<const uint4*>(kn + (tid & 7) * 16);
+            zk1 = *reinterpret_cast<const uint4*>(kn + (tid & 7) * 16 + 8);
+        }
         uint4 wv[kUIter];
         float qf[kUIter];
 #pragma unroll
@@ -366,6 +381,15 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
             const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
             const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
             u[c] = (r0 + r1) + (r2 + r3);
+        }
+        if (z_early) {
+            float z = 0.0f;
+            z = dot2_bf16(zw0.x, zk0.x, z); z = dot2_bf16(zw0.y, zk0.y, z);
+            z = dot2_bf16(zw0.z, zk0.z, z); z = dot2_bf16(zw0.w, zk0.w, z);
+            z = dot2_bf16(zw1.x, zk1.x, z); z = dot2_bf16(zw1.y, zk1.y, z);
+            z = dot2_bf16(zw1.z, zk1.z, z); z = dot2_bf16(zw1.w, zk1.w, z);
+            z = sum8(z);
+            if ((tid & 7) == 0) a.zT[((size_t)bg * 32 + (tid >> 3)) * a.C + a.write_col] = f32_to_bf16_rne(z);
         }
     }
     if (a.hist) clear_histogram<256>(hsh);
@@ -434,7 +458,7 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
         if (s + 1 < NSUB) __syncthreads();   // part is rewritten by the next sub-tile
     }
     if (tile == 0) {
-        if (a.k_new) write_z<256>(a, bg, g);
+        if (a.k_new && !z_early) write_z<256>(a, bg, g);
         if (a.u_out && lane < 8) {
             float uo = u[0];
 #pragma unroll
