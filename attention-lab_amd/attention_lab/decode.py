@@ -280,8 +280,10 @@ def sparse_decode_step_kernel(q_main, q_pre, k_cache, v_cache, zT, wq_t_scaled, 
     out = torch.empty(B, G, h, d, dtype=torch.bfloat16, device=k_cache.device)
     flat = torch.empty(B * G * S, dtype=torch.int64, device=k_cache.device) if return_rows else None
     entry = "attnlab_sparse_decode_step" if idx_dt == torch.bfloat16 else "attnlab_sparse_decode_step_f32"
+    # contiguous copies (if any) are held here: a temporary's memory could go to the next one before the launch
+    wq_c, wk_c = wq_t_scaled.contiguous(), wk.contiguous()
     nat.call(entry, q.data_ptr(), q_cat.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-             zT.data_ptr(), wq_t_scaled.contiguous().data_ptr(), wk.contiguous().data_ptr(), nat.ptr(k_new), B, G, h, r,
+             zT.data_ptr(), wq_c.data_ptr(), wk_c.data_ptr(), nat.ptr(k_new), B, G, h, r,
              C, lo, hi, legal, k, wc, sc, order, P, state.data_ptr(), ws.data_ptr(), ws.numel(), None, nat.ptr(flat),
              out.data_ptr(), nat.stream_of(k_cache.device))
     out = out.view(B, G, h, 1, d)
