@@ -14,7 +14,8 @@ import threading
 import torch
 
 LIB_NAME = "libattnlab.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# ATTNLAB_LIB names another build of the same library (the host-sanitized debug build); unset, the in-tree one
+LIB_PATH = os.environ.get("ATTNLAB_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 8
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), 64 super-bin counts of 32 bins each, then 64 arrival counters of the step's attend partitions
