@@ -124,17 +124,15 @@ __device__ __forceinline__ void write_z(const ScoreArgs& a, int bg, int g) {
     const uint16_t* kn = a.k_new + (size_t)bg * a.d;
     if (a.d == 128 && a.r <= BLOCK / 8 && ((reinterpret_cast<uintptr_t>(a.wk) | reinterpret_cast<uintptr_t>(kn)) & 15) == 0) {
         const int j = tid >> 3, e0 = (tid & 7) * 16;
-        float s = 0.0f;
+        uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0, k0 = w0, k1 = w0;
         if (j < a.r) {
             const uint16_t* wr = a.wk + ((size_t)g * a.r + j) * 128 + e0;
-            const uint4 w0 = *reinterpret_cast<const uint4*>(wr), w1 = *reinterpret_cast<const uint4*>(wr + 8);
-            const uint4 k0 = *reinterpret_cast<const uint4*>(kn + e0), k1 = *reinterpret_cast<const uint4*>(kn + e0 + 8);
-            s = dot2_bf16(w0.x, k0.x, s); s = dot2_bf16(w0.y, k0.y, s);
-            s = dot2_bf16(w0.z, k0.z, s); s = dot2_bf16(w0.w, k0.w, s);
-            s = dot2_bf16(w1.x, k1.x, s); s = dot2_bf16(w1.y, k1.y, s);
-            s = dot2_bf16(w1.z, k1.z, s); s = dot2_bf16(w1.w, k1.w, s);
+            w0 = *reinterpret_cast<const uint4*>(wr);
+            w1 = *reinterpret_cast<const uint4*>(wr + 8);
+            k0 = *reinterpret_cast<const uint4*>(kn + e0);
+            k1 = *reinterpret_cast<const uint4*>(kn + e0 + 8);
         }
-        s = sum8(s);
+        const float s = z_dot16(w0, w1, k0, k1);
         if ((tid & 7) == 0 && j < a.r) a.zT[((size_t)bg * a.r + j) * a.C + a.write_col] = f32_to_bf16_rne(s);
         return;
     }
@@ -334,7 +332,8 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
     u32x4_t vb[kDepth][8];
     // The z column (tile 0) in a grid of at most one workgroup per CU: its loads go out first and its dot products
     // follow u, so that the tile-0 workgroups do not end a memory round trip after the others (B=1, 32K: score 7.45 ->
-    // 7.23 us). Larger grids keep it at the end (no gain there; at B=16 the early form cost 0.5 us), as do other
+    // 7.23 us). Larger grids keep it at the end (no gain there; at B=16 the early form cost 0.5 us, and the column spread
+    // over the row's workgroups, ceil(32 / tiles) index rows each with the prologue, gained nothing), as do other
     // layouts (write_z).
     const uint16_t* kn = a.k_new ? a.k_new + (size_t)bg * a.d : nullptr;
     const bool z_early = !PROBE && tile == 0 && gridDim.x <= 256 && kn != nullptr && a.d == 128 &&
@@ -383,12 +382,7 @@ __global__ __launch_bounds__(256) void score_scan_fused(ScoreArgs a) {
             u[c] = (r0 + r1) + (r2 + r3);
         }
         if (z_early) {
-            float z = 0.0f;
-            z = dot2_bf16(zw0.x, zk0.x, z); z = dot2_bf16(zw0.y, zk0.y, z);
-            z = dot2_bf16(zw0.z, zk0.z, z); z = dot2_bf16(zw0.w, zk0.w, z);
-            z = dot2_bf16(zw1.x, zk1.x, z); z = dot2_bf16(zw1.y, zk1.y, z);
-            z = dot2_bf16(zw1.z, zk1.z, z); z = dot2_bf16(zw1.w, zk1.w, z);
-            z = sum8(z);
+            const float z = z_dot16(zw0, zw1, zk0, zk1);
             if ((tid & 7) == 0) a.zT[((size_t)bg * 32 + (tid >> 3)) * a.C + a.write_col] = f32_to_bf16_rne(z);
         }
     }

@@ -309,6 +309,19 @@ inline ScoreLists list_layout(void* base, int R, FusedGeometry g, ListPlan p) {
                       p.cap};
 }
 
+// One index row's z value at d = 128: of the eight threads of a row, thread t % 8 takes dims 16 (t % 8) .. + 15 (two
+// 16-byte words of wk[g, j] and of k_new) as a chain of eight bf16 dot2 from zero, then sum8 adds the eight partial
+// sums. Every writer of a z column (write_z and the score kernel's early forms) uses this order, so a column has the
+// same bits whichever workgroup writes it. Called by all lanes of the wave (sum8 exchanges).
+__device__ __forceinline__ float z_dot16(uint4 w0, uint4 w1, uint4 k0, uint4 k1) {
+    float s = 0.0f;
+    s = dot2_bf16(w0.x, k0.x, s); s = dot2_bf16(w0.y, k0.y, s);
+    s = dot2_bf16(w0.z, k0.z, s); s = dot2_bf16(w0.w, k0.w, s);
+    s = dot2_bf16(w1.x, k1.x, s); s = dot2_bf16(w1.y, k1.y, s);
+    s = dot2_bf16(w1.z, k1.z, s); s = dot2_bf16(w1.w, k1.w, s);
+    return sum8(s);
+}
+
 // The list select of the fused decode step: from the score kernel's per-workgroup lists (and the full tile scores of
 // any list that cannot hold the row's selection), the top-k and F as attnlab_select_rows writes them; one launch.
 // scores may be null when `table` is given (its zT and u): the select then recomputes the scores of a tile whose list

@@ -209,6 +209,41 @@ def test_full_size_32k_b16_properties(gpu):
     check_out(out, ref, "32K B16")
 
 
+def score_grid(B, G, lo, hi):
+    """Workgroups of the one-launch score (8, 4 or 2 sub-tiles of 512 columns each, as many as leave 256 workgroups)."""
+    span = ((hi + 7) & ~7) - (lo & ~7)
+    blocks = B * G * ((span + 511) // 512)
+    nsub = 8 if blocks >= 2048 else 4 if blocks >= 1024 else 2 if blocks >= 512 else 1
+    return B * G * ((span + 512 * nsub - 1) // (512 * nsub))
+
+
+@pytest.mark.parametrize("B,L,canonical", [(16, 16384, True), (8, 32768, False), (16, 32768, True), (4, 32768, True)])
+def test_z_column_is_the_same_bits_whichever_kernel_writes_it(gpu, B, L, canonical):
+    """The step's score kernel writes the new key's z column at the end of its tile-0 workgroups past one workgroup per
+    CU, and ahead of the table (with u) in smaller grids. Either way the column is bit for bit the one
+    attnlab_score_grouped writes on its own (write_z), at least 99% of it is the RNE of the exact value, no other column
+    of zT changes, and the rows are bit-exact against the oracle."""
+    G, h, C = 8, 2, L + 64
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, h=h, C=C, seed=B + L)
+    z_step = zT.clone()
+    req, out, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, z_step, idx, L, 1 / 32, canonical)
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    assert (score_grid(B, G, lo, hi) > 256) == (B >= 8), "the cases cover both forms"
+    z_score = zT.clone()
+    hip_score.score_grouped(z_score, lo, hi, wk=idx.wk, q_cat=q_pre.reshape(B, G, h * 128).contiguous(),
+                            wq_t=idx.wq_t_scaled, k_new=k_pre_new.reshape(B, G, 128).contiguous(), write_col=L - 1)
+    torch.cuda.synchronize()
+    assert torch.equal(z_step, z_score), "the step's z column differs from the score kernel's"
+    _, z_bits = exact.z_column(f64(k_pre_new).reshape(B, G, 128), f64(idx.wk))
+    assert np.mean(bf16.from_torch(z_step[..., L - 1]) == z_bits) >= 0.99
+    mask = torch.ones(C, dtype=torch.bool, device=gpu)
+    mask[L - 1] = False
+    assert torch.equal(z_step[..., mask], zT[..., mask])
+    want = exact.select_rows(kernel_scores(z_step, q_pre, idx, lo, hi), lo, hi, L, req.k,
+                             order="position" if canonical else "score")
+    assert np.array_equal(pos, want)
+
+
 def test_graph_replay_matches_eager(gpu):
     """The launches of a step captured in a HIP graph: every replay equals the eager result."""
     K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=4, h=4, C=4096, seed=8)
