@@ -436,7 +436,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// two workgroups per CU: the register budget then fits without AGPRs (203 VGPRs), and one workgroup's softmax
+// two workgroups per CU: the register budget then fits without AGPRs (230 VGPRs), and one workgroup's softmax
 // hides the other's matrix-core latency (1.2-1.3x over one workgroup per CU)
 __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPaKeys * kPaKPitch];
