@@ -1722,7 +1722,7 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
                     "the list select needs the select state and the lists");
     SelectArgs a{scores, score_stride, M, k, lo, hi, legal, G, C, order, rows, rows_stride, rows_flat, nullptr, nullptr, 0,
                  state};
-    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots),
+    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub, list_lspl(geo.tiles, kSelWaves, kListSlots, lists.lmin),
                recompute ? table : TableRef{}};
     // the instance for up to four sub-tiles per score workgroup keeps fewer registers live
     if (geo.nsub <= 4) hipLaunchKernelGGL(select_lists<4>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);

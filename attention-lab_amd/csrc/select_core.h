@@ -54,12 +54,18 @@ struct ListLds {
     uint32_t (*wave_tot)[2];  // one per wave
 };
 
-// Entries per lane and list of the first round trip: the largest power of two with every list of a wave covered
-// (slots / lists per wave); slots past cap are not loaded.
-inline int list_lspl(int tiles, int waves, int slots) {
+// Entries per lane and list of the first round trip (as a power of two): the largest with every list of a wave covered
+// (slots / lists per wave), but no more 64-entry slots than cover 2 lmin entries; slots past cap are not loaded, and a
+// longer list's tail is read after the first round trip. A list holds lmin entries plus the rest of the first-digit bin
+// of its lmin-th key: for Gaussian scores 1.3 lmin on average and under 2 lmin in 999 of 1000 lists (numpy model of the
+// lists at lmin = 64, 105, 177). At 32K the limit halves B=1's first round trip to 128 entries per list (lmin = 64;
+// select 6.93 -> 6.56-6.62 us, step 21.0 -> 20.56 us per layer in alternating runs) and trims B=2's from 320 to 256
+// (lmin = 105); B=4 and up keep theirs.
+inline int list_lspl(int tiles, int waves, int slots, int lmin) {
     const int nlw = (tiles + waves - 1) / waves;
     int l = 0;
     while ((2 << l) <= slots / nlw) ++l;
+    while (l > 0 && (64 << (l - 1)) >= 2 * lmin) --l;
     return l;
 }
 
