@@ -442,7 +442,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPaKeys * kPaKPitch];
     __shared__ __attribute__((aligned(16))) uint16_t vt[128 * kPaVPitch];
     const int lin = xcd_contiguous_block();
-    const int bg = lin / a.qtiles, qt = lin - bg * a.qtiles;
+    // the query tiles of a (b, g) in reverse: the later tiles read more keys, so they are dispatched first and the
+    // short ones fill in behind them
+    const int bg = lin / a.qtiles, qt = a.qtiles - 1 - (lin - bg * a.qtiles);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 31, g = lane >> 5;

@@ -110,6 +110,9 @@ def parse_args():
     ap.add_argument("--prefill-workload", action="store_true",
                     help="short run for rocprofv3: 5 launches of the batched (prefill) lightning score at its bench "
                          "shape; prints one JSON line")
+    ap.add_argument("--prefill-attend-workload", action="store_true",
+                    help="causal prefill attention (attnlab_prefill_attend) at a whole 8K prompt (h = 2, 4), a 1K "
+                         "chunk after a 7K history and B=16 x 2K; prints one JSON line")
     ap.add_argument("--index-build-workload", action="store_true",
                     help="instead of the bench line: the bulk index-table build (project_keys, bf16 and float32) "
                          "at B=16, G=8, T=32768, d=128, r=32, 10 HIP-event-timed launches each; one JSON line (also "
@@ -569,6 +572,59 @@ def index_build_workload(torch, dev, reps=10, B=16, G=8, T=32768, d=128, r=32):
         out[name] = {"avg_launch_us": us, "algorithmic_bytes": nbytes, "gbs": nbytes / us / 1e3,
                      "hbm_frac": nbytes / us / 1e3 / PEAK_HBM_GBS}
         del k_pre, wk, zT
+        torch.cuda.empty_cache()
+    print(json.dumps(out))
+    return 0
+
+
+PREFILL_ATTEND_SHAPES = (   # (B, G, h, T, q_pos0, legal): a whole causal prompt, a chunk after a history, a batch
+    (1, 8, 2, 8192, 0, 8192), (1, 8, 4, 8192, 0, 8192), (1, 8, 2, 1024, 7168, 8192), (16, 8, 2, 2048, 0, 2048))
+
+
+def prefill_attend_workload(torch, dev, reps=10, rounds=5):
+    """Causal prefill attention (attnlab_prefill_attend, the full read of full.py:17-44 for a chunk of consecutive
+    queries): per shape, 0.3 s of untimed launches, then `rounds` timed runs of `reps` back-to-back launches after two
+    untimed ones (HIP events on the launching stream), the median run per launch. Algorithmic flops: 4 d per (query, head, visible key): the two
+    products of every score."""
+    from attention_lab import _native as nat
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    out = {"prefill_attend_workload": "causal, d=128, bf16, scale 1/sqrt(d)", "launches_per_run": reps}
+    for (B, G, h, T, p0, legal) in PREFILL_ATTEND_SHAPES:
+        C, d = legal, 128
+        q = torch.randn(B, G, h, T, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        K = torch.randn(B, G, C, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        V = torch.randn(B, G, C, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        o = torch.empty_like(q)
+
+        def launch():
+            nat.call("attnlab_prefill_attend", q.data_ptr(), K.data_ptr(), V.data_ptr(), C * d, d, o.data_ptr(), B, G, h,
+                     T, d, p0, legal, C, 1.0 / math.sqrt(d), stream)
+        t_warm = time.perf_counter()   # the clocks settle over the first tens of milliseconds of launches
+        while time.perf_counter() - t_warm < 0.3:
+            for _ in range(reps):
+                launch()
+            torch.cuda.synchronize()
+        runs = []
+        for _ in range(rounds):
+            for _ in range(2):
+                launch()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                launch()
+            e1.record()
+            torch.cuda.synchronize()
+            runs.append(e0.elapsed_time(e1) * 1e3 / reps)
+        us = statistics.median(runs)
+        flops = B * G * h * sum(min(legal, p0 + t + 1) for t in range(T)) * 4 * d
+        out[f"B{B}_G{G}_h{h}_T{T}_after{p0}"] = {"avg_launch_us": us, "runs_us": runs, "flops": flops,
+                                                  "tflops": flops / us / 1e6,
+                                                  "mfma_frac_of_peak": flops / us / 1e6 / PEAK_MFMA_F16_TFLOPS}
+        print(f"[prefill_attend] B={B} G={G} h={h} T={T} after {p0}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s",
+              file=sys.stderr, flush=True)
+        del q, K, V, o
         torch.cuda.empty_cache()
     print(json.dumps(out))
     return 0
@@ -1522,6 +1578,8 @@ def main() -> int:
         return prefill_workload(torch, dev)
     if args.index_build_workload:
         return index_build_workload(torch, dev)
+    if args.prefill_attend_workload:
+        return prefill_attend_workload(torch, dev)
     if args.sweeps:
         return run_sweeps(torch, dev, args.sweeps)
     if args.c4:
