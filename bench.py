@@ -730,13 +730,31 @@ def sweep_lightning_topk(torch, dev, emit):
                         nat.call("attnlab_topk", sc[i].data_ptr(), L, B * KG, L, k, nat.ORDER_SCORE, idx.data_ptr(),
                                  val.data_ptr(), k, stream())
                 us_topk = time_rotating(torch, select, copies)
+
+                def torch_topk(i):   # the reference's own top-k (decode.py:86-93) on the same rows, for comparison
+                    torch.topk(sc[i], k, dim=-1, sorted=True)
+                try:   # graph replays time the GPU work; eager launches where torch.topk cannot be captured
+                    us_torch, torch_mode = time_rotating(torch, torch_topk, copies), "graph"
+                except RuntimeError:
+                    torch.cuda.synchronize()
+                    torch_topk(0)
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for rep in range(10):
+                        for i in range(copies):
+                            torch_topk(i)
+                    e1.record()
+                    torch.cuda.synchronize()
+                    us_torch, torch_mode = e0.elapsed_time(e1) * 1e3 / (10 * copies), "eager"
                 score_bytes = B * KG * (L * 64 + L * 4) + B * KG * nh * (32 * 4 + 4)
                 topk_bytes = B * KG * (4 * L + 8 * k)
                 emit({"sweep": "lightning_score_topk", "batch": B, "key_groups": KG, "L": L, "k": k,
                       "topk_kernels": "tiled (histogram, classify, resolve)" if tiled else "one workgroup per row",
                       "score_us": us_score, "score_gbs": score_bytes / us_score / 1e3,
                       "score_frac": score_bytes / us_score / 1e3 / PEAK_HBM_GBS,
-                      "topk_us": us_topk, "topk_gbs": topk_bytes / us_topk / 1e3})
+                      "topk_us": us_topk, "topk_gbs": topk_bytes / us_topk / 1e3, "torch_topk_us": us_torch,
+                      "torch_topk_timing": torch_mode})
                 del keys, sc
                 torch.cuda.empty_cache()
 
