@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libattnlab.so"
 # ATTNLAB_LIB names another build of the same library (the host-sanitized debug build); unset, the in-tree one
 LIB_PATH = os.environ.get("ATTNLAB_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 # select state per (b, g) row: the first-digit histogram of the top-k (2048 bins, top 11 bits of the order-preserving
 # score key), 64 super-bin counts of 32 bins each, then 64 arrival counters of the step's attend partitions
 # (ATTNLAB_SELECT_STATE_WORDS)
@@ -52,6 +52,8 @@ SIGNATURES = {
     "attnlab_dense_decode": (_i, [_p, _p, _i64, _i, _p] + [_i] * 6 + [_f, _p, _i, _p, _p]),
     "attnlab_attend_paged": (_i, [_p, _p, _i, _i, _p, _i64, _i, _p, _p, _i64] + [_i] * 5 + [_f, _p, _i, _p, _p]),
     "attnlab_prefill_attend": (_i, [_p, _p, _p, _i64, _i, _p] + [_i] * 8 + [_f, _p]),
+    "attnlab_prefill_part_bytes": (_i64, [_i] * 5),
+    "attnlab_prefill_attend_split": (_i, [_p, _p, _p, _i64, _i, _p] + [_i] * 8 + [_f, _i, _p, _i64, _p]),
     "attnlab_sparse_decode_workspace": (_i64, [_i] * 8),
     "attnlab_sparse_decode_step": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
     "attnlab_sparse_decode_step_f32": (_i, [_p] * 8 + [_i] * 10 + [_f, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),

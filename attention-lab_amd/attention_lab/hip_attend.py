@@ -327,9 +327,27 @@ def dense_decode(q, k, v, valid_length: int, *, scale=None, partitions=None, out
 PREFILL_HEADS = (1, 2, 4, 8, 16)
 
 
-def prefill_attend(q, k, v, q_pos0: int, valid_length: int, *, scale=None, out=None):
+PREFILL_ROWS = 128          # (query, head) rows per workgroup of the prefill kernel
+PREFILL_MAX_SPLITS = 16
+
+
+def prefill_splits(B: int, G: int, h: int, T: int, q_pos0: int, valid_length: int) -> int:
+    """Key splits of the causal prefill read: none once the query tiles give a workgroup per CU (256); below that as
+    many as bring the grid to about two workgroups per CU, each split at least 512 keys of the longest tile's visible
+    range. A 1K chunk after 7K cached positions at B=1, G=8, h=2 (128 tiles) takes 4."""
+    tiles = B * G * -(-T // (PREFILL_ROWS // h))
+    if tiles >= 256:
+        return 1
+    keys = min(valid_length, q_pos0 + T)
+    s = min(PREFILL_MAX_SPLITS, 512 // max(tiles, 1), keys // 512)
+    return s if s >= 2 else 1
+
+
+def prefill_attend(q, k, v, q_pos0: int, valid_length: int, *, scale=None, out=None, splits=None, workspace=None):
     """Causal prefill read on the matrix cores: q [B,G,h,T,d] at positions q_pos0 .. q_pos0 + T - 1, k/v [B,G,C,d];
-    query t reads the cache rows j <= q_pos0 + t, j < valid_length. Returns bf16 [B,G,h,T,d]."""
+    query t reads the cache rows j <= q_pos0 + t, j < valid_length. Returns bf16 [B,G,h,T,d]. A grid too small to fill
+    the chip splits each tile's keys (prefill_splits; `splits` overrides it) and merges the splits' partials, held in
+    the workspace, in a second kernel."""
     if k.dim() != 4 or k.dtype != torch.bfloat16 or not k.is_contiguous() or not k.is_cuda:
         raise ValueError("the cache must be a contiguous bfloat16 [B, G, C, d] tensor on a HIP device")
     if v.shape != k.shape or v.dtype != k.dtype or not v.is_contiguous() or v.device != k.device:
@@ -351,6 +369,16 @@ def prefill_attend(q, k, v, q_pos0: int, valid_length: int, *, scale=None, out=N
     elif out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(q.shape) or not out.is_contiguous():
         raise ValueError("out must be a contiguous bfloat16 tensor shaped like q")
     sc = float(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
-    nat.call("attnlab_prefill_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), C * d, d, out.data_ptr(), B, G, h, T,
-             d, p0, L, C, sc, nat.stream_of(k.device))
+    ns = prefill_splits(B, G, h, T, p0, L) if splits is None else int(splits)
+    if not 1 <= ns <= PREFILL_MAX_SPLITS:
+        raise ValueError(f"splits must be in [1, {PREFILL_MAX_SPLITS}]")
+    if ns == 1:
+        nat.call("attnlab_prefill_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), C * d, d, out.data_ptr(), B, G, h,
+                 T, d, p0, L, C, sc, nat.stream_of(k.device))
+        return out
+    nbytes = nat.lib().attnlab_prefill_part_bytes(B, G, h, T, ns)
+    ws = _SHARED_WS if workspace is None else workspace
+    part = ws.bytes(k.device, nbytes, "prefill_part")
+    nat.call("attnlab_prefill_attend_split", q.data_ptr(), k.data_ptr(), v.data_ptr(), C * d, d, out.data_ptr(), B, G,
+             h, T, d, p0, L, C, sc, ns, part.data_ptr(), int(part.numel()), nat.stream_of(k.device))
     return out

@@ -413,7 +413,13 @@ struct PrefillAttendArgs {
     int h, T, q_pos0, legal;
     int qtiles;             // ceil(T / (128 / h))
     float scale_log2;
+    // key split (a grid too small to fill the chip): workgroup (bg, qt, sp) reads the keys [sp kspan, (sp + 1) kspan)
+    // of its tile and writes its rows' (m, l, o) to part [BG, h, T, splits, 132] instead of out; splits == 1: none
+    int splits = 1, kspan = 0;
+    float* part = nullptr;
 };
+constexpr int kPaPart = 132;   // m, l, two unused words (16-byte aligned rows), the 128 unnormalised outputs
+constexpr int kPrefillMaxSplits = 16;
 
 constexpr int kPaRows = 128;          // (query, head) rows per workgroup: 4 waves x 32
 constexpr int kPaKeys = 64;           // keys per block
@@ -438,13 +444,17 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
 
 // two workgroups per CU: the register budget then fits without AGPRs (230 VGPRs), and one workgroup's softmax
 // hides the other's matrix-core latency (1.2-1.3x over one workgroup per CU)
+template <bool SPLIT>   // SPLIT: a.splits > 1, partials to a.part (the one-pass instance keeps no split logic)
 __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPaKeys * kPaKPitch];
     __shared__ __attribute__((aligned(16))) uint16_t vt[128 * kPaVPitch];
     const int lin = xcd_contiguous_block();
     // the query tiles of a (b, g) in reverse: the later tiles read more keys, so they are dispatched first and the
-    // short ones fill in behind them
-    const int bg = lin / a.qtiles, qt = a.qtiles - 1 - (lin - bg * a.qtiles);
+    // short ones fill in behind them; the key splits of a tile are adjacent
+    const int nsp = SPLIT ? a.splits : 1;
+    const int per_bg = a.qtiles * nsp;
+    const int bg = lin / per_bg, rem = lin - bg * per_bg;
+    const int qt = a.qtiles - 1 - rem / nsp, sp = rem - (rem / nsp) * nsp;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 31, g = lane >> 5;
@@ -460,7 +470,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(qr + 16 * kk));
     }
-    const int kend = min(a.legal, a.q_pos0 + min(t0 + BQ, a.T));                          // keys of the workgroup
+    // keys of the workgroup: its tile's visible keys, or this split's share of them
+    const int kend_tile = min(a.legal, a.q_pos0 + min(t0 + BQ, a.T));
+    const int kb0 = SPLIT ? sp * a.kspan : 0;
+    const int kend = SPLIT ? min(kend_tile, kb0 + a.kspan) : kend_tile;
     const int wave_first = a.q_pos0 + min(t0 + (32 * wave) / a.h, a.T - 1);
     const int kend_wave = min(a.legal, a.q_pos0 + min(t0 + (32 * wave + 31) / a.h, a.T - 1) + 1);
 
@@ -520,9 +533,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] = 0.0f;
 
-    gload(0);
-    for (int kb = 0; kb < kend; kb += kPaKeys) {
-        if (kb) __syncthreads();   // the previous block's LDS reads are done
+    if (kb0 < kend) gload(kb0);
+    for (int kb = kb0; kb < kend; kb += kPaKeys) {
+        if (kb != kb0) __syncthreads();   // the previous block's LDS reads are done
         lds_store();
         __syncthreads();
         if (kb + kPaKeys < kend) gload(kb + kPaKeys);
@@ -599,6 +612,20 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
     }
     const float l_tot = l_run + shfl_xor_f32(l_run, 32);
     if (t >= a.T) return;
+    if constexpr (SPLIT) {   // this split's partial: m (log2 domain, scaled), l and the unnormalised outputs
+        float* pp = a.part + ((((size_t)bg * a.h + head) * a.T + t) * a.splits + sp) * kPaPart;
+        if (g == 0) {
+            pp[0] = m_run;
+            pp[1] = l_tot;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4)
+                *reinterpret_cast<float4*>(pp + 4 + 32 * dt + 8 * i4 + 4 * g) =
+                    make_float4(o[dt][4 * i4], o[dt][4 * i4 + 1], o[dt][4 * i4 + 2], o[dt][4 * i4 + 3]);
+        return;
+    }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t* orow = a.out + (((size_t)bg * a.h + head) * a.T + t) * 128;
 #pragma unroll
@@ -610,6 +637,34 @@ __global__ __launch_bounds__(256, 2) void prefill_attend(PrefillAttendArgs a) {
                 u32x2v_t{pack_bf16x2(od[4 * i4] * inv, od[4 * i4 + 1] * inv),
                          pack_bf16x2(od[4 * i4 + 2] * inv, od[4 * i4 + 3] * inv)};
         }
+}
+
+// The key splits' partials of every (b, g, head, query) row merged into out: thread -> (row, four dims); the partials
+// are read in split order with one rescale to their largest m (the arithmetic of the non-split kernel's
+// normalisation: out = o * (1 / l), zero where no key is visible).
+__global__ __launch_bounds__(256) void prefill_combine(PrefillAttendArgs a, int64_t rows) {
+    const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (item >= rows * 32) return;
+    const int64_t row = item >> 5;
+    const int d4 = 4 * (int)(item & 31);
+    const float* pp = a.part + row * a.splits * kPaPart;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, pp[sp * kPaPart]);
+    float l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int sp = 0; sp < a.splits; ++sp) {
+        const float m = pp[sp * kPaPart];
+        const float w = m == -INFINITY ? 0.0f : fast_exp2(m - mx);
+        const float4 v = *reinterpret_cast<const float4*>(pp + sp * kPaPart + 4 + d4);
+        l += w * pp[sp * kPaPart + 1];
+        o.x += w * v.x;
+        o.y += w * v.y;
+        o.z += w * v.z;
+        o.w += w * v.w;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    *reinterpret_cast<uint2*>(a.out + row * 128 + d4) =
+        make_uint2(pack_bf16x2(o.x * inv, o.y * inv), pack_bf16x2(o.z * inv, o.w * inv));
 }
 
 }  // namespace
@@ -684,26 +739,70 @@ extern "C" int attnlab_score_lightning_batched(const uint16_t* keys, int key_dty
     return check_launch("lightning_batched");
 }
 
-extern "C" int attnlab_prefill_attend(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride,
-                                      int kv_row_stride, uint16_t* out, int B, int G, int h, int T, int d,
-                                      int q_pos0, int legal, int C, float scale, void* stream) {
+namespace {
+
+int prefill_attend_impl(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int kv_row_stride,
+                        uint16_t* out, int B, int G, int h, int T, int d, int q_pos0, int legal, int C, float scale,
+                        int splits, float* part, int64_t part_bytes, void* stream) {
     ATTNLAB_REQUIRE(B >= 1 && G >= 1 && T >= 0, "B, G must be positive and T >= 0 (B=%d G=%d T=%d)", B, G, T);
     ATTNLAB_REQUIRE(d == 128, "head_dim must be 128, got %d", d);
     ATTNLAB_REQUIRE(h == 1 || h == 2 || h == 4 || h == 8 || h == 16, "query heads per group h=%d must divide 128 "
                     "(1, 2, 4, 8 or 16)", h);
     ATTNLAB_REQUIRE(q_pos0 >= 0 && 0 < legal && legal <= C, "need q_pos0 >= 0 and 0 < legal <= C (q_pos0=%d "
                     "legal=%d C=%d)", q_pos0, legal, C);
+    ATTNLAB_REQUIRE(1 <= splits && splits <= kPrefillMaxSplits, "key splits %d outside [1, %d]", splits,
+                    kPrefillMaxSplits);
     if (T == 0) return ATTNLAB_OK;
     ATTNLAB_REQUIRE(q && K && V && out, "q, K, V and out are required");
     ATTNLAB_REQUIRE(kv_row_stride >= 128 && kv_row_stride % 8 == 0 && kv_bg_stride % 8 == 0 &&
                         ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(K) |
                           reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
                     "q, K, V, out and the K/V rows must be 16-byte aligned");
+    const int64_t need = attnlab_prefill_part_bytes(B, G, h, T, splits);
+    ATTNLAB_REQUIRE(splits == 1 || (part != nullptr && (reinterpret_cast<uintptr_t>(part) & 15) == 0 && part_bytes >= need),
+                    "%d key splits need a 16-byte aligned part buffer of attnlab_prefill_part_bytes = %lld bytes",
+                    splits, (long long)need);
     PrefillAttendArgs a{q, K, V, kv_bg_stride, kv_row_stride, out, h, T, q_pos0, legal, 0, scale * kLog2e};
     const int BQ = kPaRows / h;
     a.qtiles = (T + BQ - 1) / BQ;
-    const int64_t blocks = (int64_t)B * G * a.qtiles;
+    if (splits > 1) {
+        // every split a whole number of 64-key blocks of the longest tile's visible keys
+        const int kmax = min(legal, q_pos0 + T);
+        a.splits = splits;
+        a.kspan = ((kmax + splits - 1) / splits + kPaKeys - 1) / kPaKeys * kPaKeys;
+        a.part = part;
+    }
+    const int64_t blocks = (int64_t)B * G * a.qtiles * a.splits;
     ATTNLAB_REQUIRE(blocks < (int64_t)1 << 31, "grid of %lld workgroups is too large", (long long)blocks);
-    hipLaunchKernelGGL(prefill_attend, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (splits > 1) {
+        hipLaunchKernelGGL(prefill_attend<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+        const int64_t rows = (int64_t)B * G * h * T;
+        hipLaunchKernelGGL(prefill_combine, dim3((unsigned)((rows * 32 + 255) / 256)), dim3(256), 0, s, a, rows);
+    } else {
+        hipLaunchKernelGGL(prefill_attend<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    }
     return check_launch("prefill_attend");
+}
+
+}  // namespace
+
+extern "C" int64_t attnlab_prefill_part_bytes(int B, int G, int h, int T, int splits) {
+    if (B < 1 || G < 1 || h < 1 || T < 0 || splits < 1) return -1;
+    return splits > 1 ? (int64_t)B * G * h * T * splits * kPaPart * 4 : 0;
+}
+
+extern "C" int attnlab_prefill_attend(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride,
+                                      int kv_row_stride, uint16_t* out, int B, int G, int h, int T, int d,
+                                      int q_pos0, int legal, int C, float scale, void* stream) {
+    return prefill_attend_impl(q, K, V, kv_bg_stride, kv_row_stride, out, B, G, h, T, d, q_pos0, legal, C, scale, 1,
+                               nullptr, 0, stream);
+}
+
+extern "C" int attnlab_prefill_attend_split(const uint16_t* q, const uint16_t* K, const uint16_t* V,
+                                            int64_t kv_bg_stride, int kv_row_stride, uint16_t* out, int B, int G,
+                                            int h, int T, int d, int q_pos0, int legal, int C, float scale, int splits,
+                                            float* part, int64_t part_bytes, void* stream) {
+    return prefill_attend_impl(q, K, V, kv_bg_stride, kv_row_stride, out, B, G, h, T, d, q_pos0, legal, C, scale,
+                               splits, part, part_bytes, stream);
 }

@@ -24,7 +24,7 @@ int check_launch(const char* what) {
 
 }  // namespace attnlab
 
-extern "C" int attnlab_abi_version(void) { return 8; }
+extern "C" int attnlab_abi_version(void) { return 9; }
 
 extern "C" const char* attnlab_last_error(void) { return attnlab::g_error; }
 

@@ -587,20 +587,24 @@ def prefill_attend_workload(torch, dev, reps=10, rounds=5):
     untimed ones (HIP events on the launching stream), the median run per launch. Algorithmic flops: 4 d per (query, head, visible key): the two
     products of every score."""
     from attention_lab import _native as nat
+    from attention_lab import hip_attend
     stream = torch.cuda.current_stream(dev).cuda_stream
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    out = {"prefill_attend_workload": "causal, d=128, bf16, scale 1/sqrt(d)", "launches_per_run": reps}
+    out = {"prefill_attend_workload": "causal, d=128, bf16, scale 1/sqrt(d); key splits by hip_attend.prefill_splits "
+                                      "(the split read's merge kernel included in the time)", "launches_per_run": reps}
     for (B, G, h, T, p0, legal) in PREFILL_ATTEND_SHAPES:
         C, d = legal, 128
         q = torch.randn(B, G, h, T, d, device=dev, dtype=torch.bfloat16, generator=gen)
         K = torch.randn(B, G, C, d, device=dev, dtype=torch.bfloat16, generator=gen)
         V = torch.randn(B, G, C, d, device=dev, dtype=torch.bfloat16, generator=gen)
         o = torch.empty_like(q)
+        splits = hip_attend.prefill_splits(B, G, h, T, p0, legal)   # the wrapper's rule (full_attention, T > 1)
+        part = torch.empty(max(nat.lib().attnlab_prefill_part_bytes(B, G, h, T, splits), 16) // 4, device=dev)
 
         def launch():
-            nat.call("attnlab_prefill_attend", q.data_ptr(), K.data_ptr(), V.data_ptr(), C * d, d, o.data_ptr(), B, G, h,
-                     T, d, p0, legal, C, 1.0 / math.sqrt(d), stream)
+            nat.call("attnlab_prefill_attend_split", q.data_ptr(), K.data_ptr(), V.data_ptr(), C * d, d, o.data_ptr(),
+                     B, G, h, T, d, p0, legal, C, 1.0 / math.sqrt(d), splits, part.data_ptr(), part.numel() * 4, stream)
         t_warm = time.perf_counter()   # the clocks settle over the first tens of milliseconds of launches
         while time.perf_counter() - t_warm < 0.3:
             for _ in range(reps):
@@ -619,12 +623,13 @@ def prefill_attend_workload(torch, dev, reps=10, rounds=5):
             runs.append(e0.elapsed_time(e1) * 1e3 / reps)
         us = statistics.median(runs)
         flops = B * G * h * sum(min(legal, p0 + t + 1) for t in range(T)) * 4 * d
-        out[f"B{B}_G{G}_h{h}_T{T}_after{p0}"] = {"avg_launch_us": us, "runs_us": runs, "flops": flops,
+        out[f"B{B}_G{G}_h{h}_T{T}_after{p0}"] = {"avg_launch_us": us, "runs_us": runs, "flops": flops, "splits": splits,
                                                   "tflops": flops / us / 1e6,
                                                   "mfma_frac_of_peak": flops / us / 1e6 / PEAK_MFMA_F16_TFLOPS}
-        print(f"[prefill_attend] B={B} G={G} h={h} T={T} after {p0}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s",
+        print(f"[prefill_attend] B={B} G={G} h={h} T={T} after {p0} (splits {splits}): {us:.1f} us, "
+              f"{flops / us / 1e6:.0f} TFLOP/s",
               file=sys.stderr, flush=True)
-        del q, K, V, o
+        del q, K, V, o, part
         torch.cuda.empty_cache()
     print(json.dumps(out))
     return 0

@@ -282,6 +282,20 @@ int attnlab_prefill_attend(const uint16_t* q, const uint16_t* K, const uint16_t*
                            int C, float scale, void* stream);
 
 /*
+ * The same read with the keys of every query tile split into `splits` (1..16) ranges of whole 64-key blocks, for
+ * grids that one workgroup per tile leaves mostly idle: a short chunk after a long history, as the reference's chunked
+ * prefill runs (qwen_wrap.py:320-324 calls full_attention per chunk). Each split writes its rows' partial (running
+ * max, sum, unnormalised outputs) to `part`, a second kernel merges them into `out` in split order. The result equals
+ * attnlab_prefill_attend's up to the summation order. part: 16-byte aligned, at least attnlab_prefill_part_bytes
+ * bytes, no initialisation; splits == 1 takes no part and is attnlab_prefill_attend.
+ */
+int64_t attnlab_prefill_part_bytes(int B, int G, int h, int T, int splits);
+int attnlab_prefill_attend_split(const uint16_t* q, const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride,
+                                 int kv_row_stride, uint16_t* out, int B, int G, int h, int T, int d, int q_pos0,
+                                 int legal, int C, float scale, int splits, float* part, int64_t part_bytes,
+                                 void* stream);
+
+/*
  * Workspace (bytes) of attnlab_sparse_decode_step for these sizes: candidate scores, row list, u, tiled-select
  * scratch and split-K partials, each 256-byte aligned. Its contents need no initialisation.
  */

@@ -122,3 +122,55 @@ def test_validation(gpu):
     with pytest.raises(ValueError):   # the C ABI's own check (d must be 128)
         nat.call("attnlab_prefill_attend", q.data_ptr(), K.data_ptr(), V.data_ptr(), 16 * 128, 128, out.data_ptr(), 1,
                  1, 2, 4, 64, 0, 4, 16, 0.1, nat.stream_of(gpu))
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4, 8])
+@pytest.mark.parametrize("T,p0,cut", [(130, 1500, 9), (64, 0, 0), (300, 700, 0)])
+def test_key_splits_match_the_oracle(gpu, splits, T, p0, cut):
+    """The key-split read (attnlab_prefill_attend_split) against the float64 oracle: a chunk after a long history with a
+    cut, a chunk at position 0 (the later splits of its early tiles hold no visible key) and a chunk whose split
+    boundaries fall inside its tiles' visible ranges."""
+    B, G, h = 1, 2, 2
+    legal = p0 + T - cut
+    C = p0 + T + 5
+    K, V, q = inputs(gpu, B, G, h, T, C, seed=splits * 100 + T)
+    out = hip_attend.prefill_attend(q, K, V, p0, legal, splits=splits)
+    torch.cuda.synchronize()
+    want = exact.causal_attention(f64(q), f64(K), f64(V), legal, list(range(p0, p0 + T)))
+    check(out, want, f"splits={splits} T={T} p0={p0} legal={legal}")
+
+
+def test_key_splits_against_the_unsplit_read_and_the_rule(gpu):
+    """A 1K chunk after 7K cached positions at B=1, G=8, h=2 takes four splits by the rule; the merged output equals
+    the one-pass read up to the summation order (within two bf16 ulps of 1 here), and rows past valid_length stay
+    unread."""
+    B, G, h, T, p0 = 1, 8, 2, 1024, 7168
+    legal, C = p0 + T, p0 + T + 64
+    assert hip_attend.prefill_splits(B, G, h, T, p0, legal) == 4
+    assert hip_attend.prefill_splits(1, 8, 2, 8192, 0, 8192) == 1          # 1024 tiles: one per tile
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    K = torch.randn(B, G, C, 128, generator=gen, device=gpu).to(torch.bfloat16)
+    V = torch.randn(B, G, C, 128, generator=gen, device=gpu).to(torch.bfloat16)
+    q = torch.randn(B, G, h, T, 128, generator=gen, device=gpu).to(torch.bfloat16)
+    one = hip_attend.prefill_attend(q, K, V, p0, legal, splits=1)
+    split = hip_attend.prefill_attend(q, K, V, p0, legal)
+    K[:, :, legal:] = float("nan")
+    V[:, :, legal:] = float("nan")
+    again = hip_attend.prefill_attend(q, K, V, p0, legal)
+    torch.cuda.synchronize()
+    assert float((one.float() - split.float()).abs().max()) <= 2 ** -6
+    assert torch.equal(again, split)
+
+
+def test_key_split_validation(gpu):
+    K, V, q = inputs(gpu, 1, 1, 2, 4, 16, seed=2)
+    with pytest.raises(ValueError):
+        hip_attend.prefill_attend(q, K, V, 0, 16, splits=17)
+    out = torch.empty_like(q)
+    need = nat.lib().attnlab_prefill_part_bytes(1, 1, 2, 4, 2)
+    assert need == 1 * 1 * 2 * 4 * 2 * 132 * 4
+    part = torch.empty(need // 4 - 1, dtype=torch.float32, device=gpu)
+    with pytest.raises(ValueError):   # a part buffer one float short
+        nat.call("attnlab_prefill_attend_split", q.data_ptr(), K.data_ptr(), V.data_ptr(), 16 * 128, 128,
+                 out.data_ptr(), 1, 1, 2, 4, 128, 0, 16, 16, 0.1, 2, part.data_ptr(), (need // 4 - 1) * 4,
+                 nat.stream_of(gpu))
