@@ -124,16 +124,17 @@ def test_validation(gpu):
                  1, 2, 4, 64, 0, 4, 16, 0.1, nat.stream_of(gpu))
 
 
+@pytest.mark.parametrize("h", [1, 2, 8])
 @pytest.mark.parametrize("splits", [2, 3, 4, 8])
 @pytest.mark.parametrize("T,p0,cut", [(130, 1500, 9), (64, 0, 0), (300, 700, 0)])
-def test_key_splits_match_the_oracle(gpu, splits, T, p0, cut):
+def test_key_splits_match_the_oracle(gpu, h, splits, T, p0, cut):
     """The key-split read (attnlab_prefill_attend_split) against the float64 oracle: a chunk after a long history with a
     cut, a chunk at position 0 (the later splits of its early tiles hold no visible key) and a chunk whose split
-    boundaries fall inside its tiles' visible ranges."""
-    B, G, h = 1, 2, 2
+    boundaries fall inside its tiles' visible ranges, at 128, 64 and 16 queries per tile (h = 1, 2, 8)."""
+    B, G = 1, 2
     legal = p0 + T - cut
     C = p0 + T + 5
-    K, V, q = inputs(gpu, B, G, h, T, C, seed=splits * 100 + T)
+    K, V, q = inputs(gpu, B, G, h, T, C, seed=splits * 100 + T + h)
     out = hip_attend.prefill_attend(q, K, V, p0, legal, splits=splits)
     torch.cuda.synchronize()
     want = exact.causal_attention(f64(q), f64(K), f64(V), legal, list(range(p0, p0 + T)))
