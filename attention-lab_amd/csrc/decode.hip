@@ -108,6 +108,10 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
         rc = ATTNLAB_OK;
     }
     if (rc) return rc;
+    // no row list leaves the call: select and attend in one launch, the row list kept in LDS (the same output bits)
+    if (plan.cap > 0 && !rows_out && !rows_flat && select_attend_applies(B, G, lo, hi, legal, k, h, P))
+        return select_attend_impl(B, G, lo, hi, legal, k, C, state, lists, geo, TableRef{zT, z_dtype, C, u_ws}, K, V,
+                                  q_main, h, P, scale, out, part, s);
     if (plan.cap > 0)
         rc = select_lists_impl(store_scores ? scores : nullptr, L.score_stride, B, G, lo, hi, legal, k, C, order, rows,
                                S, rows_flat, state, lists, geo, s, TableRef{zT, z_dtype, C, u_ws});

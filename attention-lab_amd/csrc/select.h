@@ -338,6 +338,19 @@ int attend_impl(const uint16_t* K, const uint16_t* V, int64_t kv_bg_stride, int 
                 const int32_t* rows, int64_t rows_stride, int B, int G, int h, int S, int C, int P, float scale,
                 void* out, int out_bf16, float* part, uint32_t* arrive, int64_t arrive_stride, hipStream_t stream);
 
+// Head groups of the attend's grid: the h heads split over 2, 4, ... workgroups while the grid is below one workgroup
+// per CU (attend.hip).
+int attend_head_groups(int BG, int h, int P);
+
+// The fused step's select and attend in one launch (select.hip: select_attend), for position order with no row list
+// leaving the call: whether it applies to these sizes (each partition's row-list entries fit its LDS, one, two or four
+// heads per workgroup), and the launch. state, lists, geo and table as for select_lists_impl; K, V [B*G, C, 128], q
+// [B*G, h, 128], out [B*G, h, 128] bf16; part [B*G, P, h, 130] for P > 1, merged in-kernel with the state's counters.
+bool select_attend_applies(int B, int G, int lo, int hi, int legal, int k, int h, int P);
+int select_attend_impl(int B, int G, int lo, int hi, int legal, int k, int C, uint32_t* state, const ScoreLists& lists,
+                       FusedGeometry geo, TableRef table, const uint16_t* K, const uint16_t* V, const uint16_t* q, int h,
+                       int P, float scale, uint16_t* out, float* part, hipStream_t stream);
+
 // attnlab_score_grouped_f32: the same score on float32 tables (trained index banks); two launches (prologue, scan).
 int score_grouped_f32_impl(float* zT, const float* k_new, const float* wk, const float* q_cat, const float* wq_t,
                            const float* u_in, float* u_out, float* out, int64_t out_stride, int B, int G, int r,

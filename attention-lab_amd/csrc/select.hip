@@ -18,6 +18,7 @@
 #include "common.h"
 #include "select.h"
 #include "select_core.h"
+#include "attend_core.h"
 
 namespace attnlab {
 
@@ -1493,6 +1494,126 @@ __global__ __launch_bounds__(kSelThreads) void select_lists(SelectArgs a, ListAr
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Select and attend in one launch (the fused step in position order when no row list leaves the call): workgroup
+// (b, g, head group qg, partition p) of the attend's grid first selects its row from the score kernel's key lists
+// (list_select_bitmap, eight waves), keeps the positions of its own partition of the row list in LDS, and then its first
+// four waves attend them exactly as attend_kernel does (the same pipeline, merges and split-K merge, so the output is
+// the same bit for bit). Every workgroup of a row computes the same selection; the last of them to have read the row's
+// first-digit bins clears them, and the attend's last partition leaves its arrival counter zero, so the select state is
+// zero again after the call. Saves the select's launch, its row-list stores and the attend's staging round trip.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int kSAThreads = 512;
+constexpr int kSAWaves = kSAThreads / 64;
+constexpr int kSASlots = 8;            // list entries per lane in the first round trip
+constexpr int kSAMaxRows = 4096;       // positions of one partition held in LDS
+constexpr int kSAReadCounter = kSelectStateWords - 1;   // the row's readers of its bins: the last arrival word
+static_assert(kListWords == 2 * kSAThreads, "two selection bitmap words per thread");
+
+template <int MAXSUB, int H>
+__global__ __launch_bounds__(kSAThreads) void select_attend(SelectArgs sa, ListArgs t, AttendArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t hist[kHistBins];
+    __shared__ __attribute__((aligned(16))) uint32_t lds[2048 + 1024 + 2 * kListWords];
+    __shared__ __attribute__((aligned(16))) uint2 cand[kListCandCap];
+    __shared__ uint2 hdr[kListMaxTiles];
+    __shared__ uint32_t sup2[64];
+    __shared__ uint32_t misc[4];
+    __shared__ uint32_t wave_tot[kSAWaves][2];
+    __shared__ float red_ml[kMergeSlots][H][2];
+    __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
+    __shared__ uint32_t last_sh, clear_sh;
+    int* idx_sh = reinterpret_cast<int*>(cand);   // the partition's positions, once the selection no longer needs cand
+    static_assert(kSAMaxRows * sizeof(int) <= sizeof(cand), "the positions fit the candidate array");
+    const int lin = xcd_contiguous_block();   // (b, g) on the XCD whose score workgroups wrote its lists
+    const int bg = lin / (a.Q * a.P);
+    const int rem = lin - bg * a.Q * a.P;
+    const int qg = rem / a.P;
+    const int p = rem - qg * a.P;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool active = tid < kAttThreads;    // the attending waves
+    const int hq = a.h / a.Q, h0 = qg * hq;
+    uint32_t qw[H][8];   // loaded first: it arrives while the selection runs
+    attend_load_q<H>(a, bg, h0, hq, qw);
+
+    ListLds L;
+    L.hist = hist;
+    L.hist2 = lds;
+    L.sup2 = sup2;
+    L.hist3 = lds + 2048;
+    L.bits = lds + 3072;
+    L.ties = lds + 3072 + kListWords;
+    L.hdr = hdr;
+    L.cand = cand;
+    L.misc = misc;
+    L.wave_tot = wave_tot;
+    ListRow r;
+    r.scores = RowScores{sa.scores ? sa.scores + (size_t)bg * sa.score_stride : nullptr, t.table, bg, sa.lo, sa.hi};
+    r.state = sa.hist + (size_t)bg * kSelectStateWords;
+    r.entries = t.entries + (size_t)bg * t.tiles * t.cap;
+    r.hdr = t.hdr + (size_t)bg * t.tiles;
+    r.M = sa.M;
+    r.k = sa.k;
+    r.lo = sa.lo;
+    r.hi = sa.hi;
+    r.cap = t.cap;
+    r.tiles = t.tiles;
+    r.nsub = t.nsub;
+    r.lspl = t.lspl;
+    list_select_bitmap<kSAThreads, kSASlots, MAXSUB>(r, L);
+    // every thread has passed the selection's first barrier, so the bins are read: count this workgroup as a reader
+    uint32_t* st = sa.hist + (size_t)bg * kSelectStateWords;
+    if (tid == 0)
+        clear_sh = __hip_atomic_fetch_add(st + kSAReadCounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(a.Q * a.P - 1);
+    // this thread's selected candidates [64 tid, 64 tid + 64) and their first slot among the k picks
+    const uint2 wv = reinterpret_cast<const uint2*>(L.bits)[tid];
+    uint64_t word = (uint64_t)wv.x | ((uint64_t)wv.y << 32);
+    const uint32_t x = (uint32_t)__popcll(word);
+    const uint32_t inc = wave_incl_scan(x);
+    if (lane == 63) wave_tot[wave][0] = inc;
+    __syncthreads();   // also: the candidates (cand) are no longer read, so idx_sh may take their place
+    const uint32_t v = lane < kSAWaves ? wave_tot[lane][0] : 0u;
+    const uint32_t vi = row16_incl_scan(v);
+    uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)(vi - v), wave) + inc - x;
+    // the partition's entries of the row list [F sinks | the k picks by position | F recent]
+    const int lo = sa.lo, k = sa.k, nrec = sa.legal - sa.hi, nf = lo + nrec;
+    const int Sp = (a.S + a.P - 1) / a.P;
+    const int s_begin = p * Sp, s_end = min(a.S, s_begin + Sp);
+    const int pos0 = lo + 64 * tid;
+    while (word) {
+        const int b = __ffsll((unsigned long long)word) - 1;
+        word &= word - 1;
+        const int e = lo + (int)slot;   // its row-list entry
+        if (slot < (uint32_t)k && e >= s_begin && e < s_end) idx_sh[e - s_begin] = pos0 + b;
+        ++slot;
+    }
+    for (int f = tid; f < nf; f += kSAThreads) {
+        const int e = f < lo ? f : lo + k + (f - lo);
+        if (e >= s_begin && e < s_end) idx_sh[e - s_begin] = f < lo ? f : sa.hi + (f - lo);
+    }
+    if (clear_sh) {   // the row's last reader: its bins and super-bins, and the reader count, back to zero
+        for (int i = tid; i < kHistBins + kSuperBins; i += kSAThreads) st[i] = 0u;
+        if (tid == 0) st[kSAReadCounter] = 0u;
+    }
+    __syncthreads();
+    float m[H], l[H], acc[H][16];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    }
+    if (active && s_end > s_begin) {
+        const size_t bg_off = (size_t)bg * a.kv_bg_stride;
+        const uint16_t* Kb = a.K + bg_off + 8 * (tid & 7);
+        const uint16_t* Vb = a.V + bg_off + 8 * (tid & 7);
+        attend_chunk<H, kStages, false, false>(a, Kb, Vb, s_begin, s_end - s_begin, idx_sh, qw, m, l, acc);
+    }
+    attend_finish<H>(a, bg, qg, p, hq, h0, m, l, acc, red_ml, red_acc, &last_sh, active);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Score order past kMaxScoreOrderK, where the k selected pairs no longer fit the LDS sort: the select runs in position
 // order into `stage` (candidate indices, ascending), then select_sort_score lists them by descending score with three
 // stable LSD radix passes over the order-preserving key (digits of 10, 11 and 11 bits, each complemented so that
@@ -1728,6 +1849,46 @@ int select_lists_impl(const float* scores, int64_t score_stride, int B, int G, i
     if (geo.nsub <= 4) hipLaunchKernelGGL(select_lists<4>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
     else hipLaunchKernelGGL(select_lists<8>, dim3(B * G), dim3(kSelThreads), 0, stream, a, t);
     return check_launch("select_lists");
+}
+
+bool select_attend_applies(int B, int G, int lo, int hi, int legal, int k, int h, int P) {
+    if (k <= 0 || hi - lo > kListMaxM || P < 1 || h < 1) return false;
+    const int S = lo + (legal - hi) + k;
+    const int Q = attend_head_groups(B * G, h, P);
+    const int hq = h / Q;
+    return (hq == 1 || hq == 2 || hq == 4) && (S + P - 1) / P <= kSAMaxRows && Q <= kSAReadCounter - kArriveOffset;
+}
+
+int select_attend_impl(int B, int G, int lo, int hi, int legal, int k, int C, uint32_t* state, const ScoreLists& lists,
+                       FusedGeometry geo, TableRef table, const uint16_t* K, const uint16_t* V, const uint16_t* q, int h,
+                       int P, float scale, uint16_t* out, float* part, hipStream_t stream) {
+    const int M = hi - lo, S = lo + (legal - hi) + k;
+    if (!select_attend_applies(B, G, lo, hi, legal, k, h, P)) return set_error(ATTNLAB_EINVAL, "select_attend: shape");
+    ATTNLAB_REQUIRE(state && lists.entries && lists.hdr && table.zT && table.u && K && V && q && out &&
+                        (P == 1 || part != nullptr),
+                    "select_attend needs the state, the lists, the table, the cache, q, out and (P > 1) partials");
+    SelectArgs sa{nullptr, 0, M, k, lo, hi, legal, G, C, ATTNLAB_ORDER_POSITION, nullptr, 0, nullptr, nullptr, nullptr, 0,
+                  state};
+    ListArgs t{lists.entries, lists.hdr, lists.cap, geo.tiles, geo.nsub,
+               list_lspl(geo.tiles, kSAWaves, kSASlots, lists.lmin), table};
+    const int Q = attend_head_groups(B * G, h, P);
+    AttendArgs a{K, V, (int64_t)C * kHeadDim, kHeadDim, q, nullptr, 0, S, C, h, P, Q, scale * kLog2e, out, 1, part};
+    if (P > 1) {
+        a.arrive = state + kArriveOffset;
+        a.arrive_stride = kSelectStateWords;
+    }
+    const dim3 grid(B * G * Q * P), block(kSAThreads);
+    const int hq = h / Q;
+#define SA_LAUNCH(MS)                                                                                     \
+    do {                                                                                                  \
+        if (hq == 1) hipLaunchKernelGGL((select_attend<MS, 1>), grid, block, 0, stream, sa, t, a);        \
+        else if (hq == 2) hipLaunchKernelGGL((select_attend<MS, 2>), grid, block, 0, stream, sa, t, a);   \
+        else hipLaunchKernelGGL((select_attend<MS, 4>), grid, block, 0, stream, sa, t, a);                \
+    } while (0)
+    if (geo.nsub <= 4) SA_LAUNCH(4);
+    else SA_LAUNCH(8);
+#undef SA_LAUNCH
+    return check_launch("select_attend");
 }
 
 int select_rows_impl(const float* scores, int64_t score_stride, int B, int G, int lo, int hi, int legal, int k, int C,

@@ -615,3 +615,46 @@ def test_in_kernel_partition_merge_equals_the_combine_kernel(gpu, G, h, P):
         want = exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), pos.cpu().numpy())
         check_out(out, want, f"G={G} P={P} call {call}")
         assert int(ws.bytes(gpu, 0, "state").abs().sum()) == 0, "arrival counters left non-zero"
+
+
+@pytest.mark.parametrize("B,G,h,C,L,rho,case,P", [
+    (1, 8, 2, 2048 + 64, 2048, 1 / 32, None, None),          # config 1
+    (1, 8, 2, 32768 + 64, 32768, 1 / 32, None, None),        # B=1 at 32K: partitions split each row
+    (16, 8, 4, 16384, 16384, 1 / 32, None, None),            # two sub-tiles per score workgroup
+    (2, 8, 4, 8192 + 64, 8192, 1 / 8, "skewed_tile", None),  # an incomplete list: its tile recomputed
+    (1, 8, 2, 16384 + 64, 16384, 1 / 16, "all_equal", None), # bin b1 past the LDS candidates: radix passes
+    (2, 8, 2, 8192 + 64, 8192, 1 / 8, "seven_values", None), # ties at the threshold
+    (1, 3, 2, 8192 + 64, 8192, 1 / 8, None, 1),
+    (1, 3, 2, 8192 + 64, 8192, 1 / 8, None, 3),              # partitions of one row on several XCDs
+    (1, 3, 4, 8192 + 64, 8192, 1 / 8, None, 16),
+    (1, 2, 1, 300, 256, 1 / 8, None, None),                  # sinks, picks and recent rows in one partition
+])
+def test_fused_select_attend_equals_the_separate_stages(gpu, B, G, h, C, L, rho, case, P):
+    """A step whose row list does not leave the call selects and attends in one launch (every workgroup of a row
+    repeats the row's selection and keeps its partition of the row list in LDS). Its output equals, bit for bit, the
+    same step run as separate select and attend launches (asking for the rows) in position order, twice in a row on one
+    workspace with other queries; the select state is zero after each call."""
+    from attention_lab import _native as nat
+    ws = nat.Workspace()
+    K, V, q, q_pre, k_pre_new, zT, idx = setup(gpu, B=B, G=G, h=h, C=C, seed=L + B + G + h)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    if case:
+        _shape_scores(zT, lo, hi, case)
+    for call in range(2):
+        if call:
+            q = torch.randn(q.shape, generator=torch.Generator().manual_seed(call)).to(torch.bfloat16).to(gpu)
+        outs = []
+        for rows in (False, True):
+            z = zT.clone()
+            got = sparse_decode_step_kernel(q, q_pre, K, V, z, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo,
+                                            lo, hi, req.k, req.selected_count, k_pre_new=k_pre_new,
+                                            write_col=req.write_col, return_rows=rows, canonical_order=True,
+                                            partitions=P, workspace=ws)
+            torch.cuda.synchronize()
+            assert int(ws.bytes(gpu, 0, "state").abs().sum()) == 0, f"rows={rows}: the select state left dirty"
+            outs.append(got[0] if rows else got)
+        assert torch.equal(outs[0], outs[1]), f"call {call}: the fused launch differs from the separate stages"
+    s = kernel_scores(zT, q_pre, idx, lo, hi)
+    want = exact.select_rows(s, lo, hi, L, req.k, order="position")
+    check_out(outs[0], exact.subset_attention(f64(q)[:, :, :, 0], f64(K), f64(V), want), f"{case} P={P}")
