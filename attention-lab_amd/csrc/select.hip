@@ -1520,7 +1520,7 @@ __global__ __launch_bounds__(kSAThreads) void select_attend(SelectArgs sa, ListA
     __shared__ uint32_t wave_tot[kSAWaves][2];
     __shared__ float red_ml[kMergeSlots][H][2];
     __shared__ __attribute__((aligned(16))) float red_acc[kMergeSlots][H][kHeadDim];
-    __shared__ uint32_t last_sh, clear_sh;
+    __shared__ uint32_t last_sh;
     int* idx_sh = reinterpret_cast<int*>(cand);   // the partition's positions, once the selection no longer needs cand
     static_assert(kSAMaxRows * sizeof(int) <= sizeof(cand), "the positions fit the candidate array");
     const int lin = xcd_contiguous_block();   // (b, g) on the XCD whose score workgroups wrote its lists
@@ -1560,11 +1560,6 @@ __global__ __launch_bounds__(kSAThreads) void select_attend(SelectArgs sa, ListA
     r.nsub = t.nsub;
     r.lspl = t.lspl;
     list_select_bitmap<kSAThreads, kSASlots, MAXSUB>(r, L);
-    // every thread has passed the selection's first barrier, so the bins are read: count this workgroup as a reader
-    uint32_t* st = sa.hist + (size_t)bg * kSelectStateWords;
-    if (tid == 0)
-        clear_sh = __hip_atomic_fetch_add(st + kSAReadCounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (uint32_t)(a.Q * a.P - 1);
     // this thread's selected candidates [64 tid, 64 tid + 64) and their first slot among the k picks
     const uint2 wv = reinterpret_cast<const uint2*>(L.bits)[tid];
     uint64_t word = (uint64_t)wv.x | ((uint64_t)wv.y << 32);
@@ -1591,11 +1586,20 @@ __global__ __launch_bounds__(kSAThreads) void select_attend(SelectArgs sa, ListA
         const int e = f < lo ? f : lo + k + (f - lo);
         if (e >= s_begin && e < s_end) idx_sh[e - s_begin] = f < lo ? f : sa.hi + (f - lo);
     }
-    if (clear_sh) {   // the row's last reader: its bins and super-bins, and the reader count, back to zero
-        for (int i = tid; i < kHistBins + kSuperBins; i += kSAThreads) st[i] = 0u;
-        if (tid == 0) st[kSAReadCounter] = 0u;
-    }
     __syncthreads();
+    if (wave == kAttWaves) {
+        // every thread has passed the selection's barriers, so this workgroup has read the row's bins: wave kAttWaves,
+        // idle while the first four attend, counts it as a reader, and the row's last reader sets the bins, the
+        // super-bins and the count back to zero (off the attend's path: its atomic's return is waited for here)
+        uint32_t* st = sa.hist + (size_t)bg * kSelectStateWords;
+        uint32_t readers = 0u;
+        if (lane == 0)
+            readers = __hip_atomic_fetch_add(st + kSAReadCounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)__builtin_amdgcn_readfirstlane((int)readers) == (uint32_t)(a.Q * a.P - 1)) {
+            for (int i = lane; i < kHistBins + kSuperBins; i += 64) st[i] = 0u;
+            if (lane == 0) st[kSAReadCounter] = 0u;
+        }
+    }
     float m[H], l[H], acc[H][16];
 #pragma unroll
     for (int i = 0; i < H; ++i) {
