@@ -1569,18 +1569,22 @@ __global__ __launch_bounds__(kSAThreads) void select_attend(SelectArgs sa, ListA
     __syncthreads();   // also: the candidates (cand) are no longer read, so idx_sh may take their place
     const uint32_t v = lane < kSAWaves ? wave_tot[lane][0] : 0u;
     const uint32_t vi = row16_incl_scan(v);
-    uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)(vi - v), wave) + inc - x;
+    const uint32_t slot = (uint32_t)__builtin_amdgcn_readlane((int)(vi - v), wave) + inc - x;
     // the partition's entries of the row list [F sinks | the k picks by position | F recent]
     const int lo = sa.lo, k = sa.k, nrec = sa.legal - sa.hi, nf = lo + nrec;
     const int Sp = (a.S + a.P - 1) / a.P;
     const int s_begin = p * Sp, s_end = min(a.S, s_begin + Sp);
     const int pos0 = lo + 64 * tid;
-    while (word) {
-        const int b = __ffsll((unsigned long long)word) - 1;
-        word &= word - 1;
-        const int e = lo + (int)slot;   // its row-list entry
-        if (slot < (uint32_t)k && e >= s_begin && e < s_end) idx_sh[e - s_begin] = pos0 + b;
-        ++slot;
+    // this thread's picks take slots [slot, slot + x) of the k (row-list entries lo + slot ..); those inside the
+    // partition, [first, last), go to LDS: the picks before it are dropped, and no lane loops over picks past it
+    const int first = max((int)slot, s_begin - lo), last = min((int)slot + (int)x, min(s_end - lo, k));
+    if (first < last) {
+        for (int j = (int)slot; j < first; ++j) word &= word - 1;
+        int* dst = idx_sh + (lo + first - s_begin);
+        for (int n = last - first; n > 0; --n) {
+            *dst++ = pos0 + (__ffsll((unsigned long long)word) - 1);
+            word &= word - 1;
+        }
     }
     for (int f = tid; f < nf; f += kSAThreads) {
         const int e = f < lo ? f : lo + k + (f - lo);
