@@ -379,16 +379,19 @@ def launchers(ls, torch):
     return {"sparse": sparse, "dense": dense, "score": score, "select": select, "attend": attend,
             "score_select": score_select, "hist": hist, "partitions": P, "attend_partitions": Pa,
             "dense_partitions": Pd,
-            "select_kernels": "select_lists" if list_bytes > 0 else "select_classify_compact + select_resolve_compact",
+            "select_kernels": "select_attend (fused with the attend)" if list_bytes > 0
+                              else "select_classify_compact + select_resolve_compact",
             "_keep": (ws, part, step_hist, u_buf, sel_scratch, lists)}
 
 
 def kernel_breakdown(torch, fns, ls, reps):
     """Per-layer us of each stage of the fused step, from graphs of one launch per layer on consistent data, each
     stage in forward and reverse layer order (median, p95, conservative): score (u, z column, scan and, where the list
-    select applies, its key lists: one kernel), select = (score + select) - score (the select consumes and clears the
+    select applies, its key lists: one kernel), select_attend = step - score (the step's second launch where the list
+    select applies: every attend workgroup selects its row and attends its partition, merging split-K partials
+    in-kernel), select = (score + select) - score (the standalone select_lists launch; it consumes and clears the
     histogram the scan builds; score-only graphs leave it dirty, so it is zeroed before the pair), attend = step -
-    (score + select) (the step's attend merges its split-K partials in-kernel), and attend_standalone, attnlab_attend
+    (score + select) (what the fused launch costs beyond a standalone select), and attend_standalone, attnlab_attend
     with the combine kernel. The flat figures are the conservative medians; `mean` holds the forward-order means (the
     kernel-trace averages compare with these)."""
     n = ls.n
@@ -399,15 +402,16 @@ def kernel_breakdown(torch, fns, ls, reps):
     step = ordered_stats(torch, fns["sparse"], n, reps, 3, per=n)
     standalone = ordered_stats(torch, fns["attend"], n, reps, 3, per=n)
     diff = lambda a, b: {o: {k: a[o][k] - b[o][k] for k in ("median_us", "mean_us")} for o in ("forward", "reverse")}
-    select, attend = diff(pair, score), diff(step, pair)
-    for x in (select, attend):
+    select, attend, fused = diff(pair, score), diff(step, pair), diff(step, score)
+    for x in (select, attend, fused):
         x["conservative_us"] = max(x["forward"]["median_us"], x["reverse"]["median_us"])
-    return {"score": score["conservative_us"], "select": select["conservative_us"], "attend": attend["conservative_us"],
+    return {"score": score["conservative_us"], "select_attend": fused["conservative_us"],
+            "select": select["conservative_us"], "attend": attend["conservative_us"],
             "attend_standalone": standalone["conservative_us"],
-            "mean": {"score": score["forward"]["mean_us"], "select": select["forward"]["mean_us"],
-                     "attend": attend["forward"]["mean_us"]},
-            "orders": {"score": score, "score_select": pair, "step": step, "select": select, "attend": attend,
-                       "attend_standalone": standalone}}
+            "mean": {"score": score["forward"]["mean_us"], "select_attend": fused["forward"]["mean_us"],
+                     "select": select["forward"]["mean_us"], "attend": attend["forward"]["mean_us"]},
+            "orders": {"score": score, "score_select": pair, "step": step, "select_attend": fused, "select": select,
+                       "attend": attend, "attend_standalone": standalone}}
 
 
 def capture(torch, fn, layers, reverse=False):
@@ -1461,7 +1465,8 @@ def run_b1(torch, dev, args):
         us = sp["conservative_us"]
         res[f"h{hpg}"] = {"sparse_us_per_layer": us, "dense_us_per_layer": dn["conservative_us"],
                           "sparse_orders": sp, "dense_orders": dn,
-                          "kernel_us": {k: per[k] for k in ("score", "select", "attend", "attend_standalone")},
+                          "kernel_us": {k: per[k] for k in ("score", "select_attend", "select", "attend",
+                                                            "attend_standalone")},
                           "sparse_algorithmic_bytes_per_layer": sparse_bytes,
                           "sparse_gbs": sparse_bytes / (us * 1e-6) / 1e9,
                           "sparse_frac_of_peak": sparse_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS}
@@ -1696,8 +1701,8 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": sb, "avg_launch_us": score_us},
         "timing": timing,
         "per_layer_us": {"sparse": us_layer, "sparse_conservative": us_layer_cons, "dense": ms_dense * 1e3 / ls.n,
-                         "score": kus["score"], "select": kus["select"], "attend": kus["attend"],
-                         "attend_standalone": kus["attend_standalone"],
+                         "score": kus["score"], "select_attend": kus["select_attend"], "select": kus["select"],
+                         "attend": kus["attend"], "attend_standalone": kus["attend_standalone"],
                          "select_kernels": fns["select_kernels"],
                          "note": "sparse: the timed region's mean; the kernel figures and dense: conservative medians "
                                  "(slower of forward / reverse layer order); kernel_orders holds every order's median, "
@@ -1707,8 +1712,9 @@ def main() -> int:
                          "frac_of_peak": sparse_bytes / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBS,
                          "frac_of_peak_conservative": sparse_bytes / (us_layer_cons * 1e-6) / 1e9 / PEAK_HBM_GBS},
         "kernels": {
+            "select_attend": {"bytes": selb + ab, "gbs": (selb + ab) / (kus["select_attend"] * 1e-6) / 1e9},
             "select": {"bytes": selb, "gbs": selb / (kus["select"] * 1e-6) / 1e9},
-            "attend": {"bytes": ab, "gbs": ab / (kus["attend"] * 1e-6) / 1e9},
+            "attend_standalone": {"bytes": ab, "gbs": ab / (kus["attend_standalone"] * 1e-6) / 1e9},
             "dense": {"bytes": db, "gbs": db / (ms_dense * 1e-3 / ls.n) / 1e9,
                       "frac": db / (ms_dense * 1e-3 / ls.n) / 1e9 / PEAK_HBM_GBS},
         },
