@@ -347,3 +347,31 @@ def test_parameter_mutation_rejects_before_cache_write(gpu, tmp_path):
         run.step(torch.tensor([[2]], device=gpu))
     assert st.cache.valid_length == length and st.cache.writes == writes
     unwrap_model(model)
+
+
+@pytest.mark.parametrize("B,h,C,L,rho,case", [(1, 2, 32768 + 64, 32768, 1 / 32, None),
+                                              (2, 4, 8192 + 64, 8192, 1 / 8, "skewed_tile"),
+                                              (1, 2, 16384 + 64, 16384, 1 / 16, "all_equal")])
+def test_step_without_rows_equals_the_separate_stages(gpu, B, h, C, L, rho, case):
+    """Over float32 tables too, a step that returns no row list selects inside the attend's workgroups: its output
+    equals, bit for bit, the same step asking for its rows in position order (separate select and attend launches),
+    incomplete lists recomputed from the float32 table included."""
+    G = 8
+    zT, q_pre, k_pre_new, idx = setup(gpu, B, G, h, C, seed=L + 7)
+    gen = torch.Generator().manual_seed(C)
+    K = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    V = torch.randn(B, G, C, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    q = torch.randn(B, G, h, 1, 128, generator=gen).to(torch.bfloat16).to(gpu)
+    req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
+    lo, hi = req.layout.candidate_lo, req.layout.candidate_hi
+    if case:
+        _shape_table(zT, lo, hi, case)
+    outs = []
+    for rows in (False, True):
+        z = zT.clone()
+        got = sparse_decode_step_kernel(q, q_pre, K, V, z, idx.wq_t_scaled, idx.wk, req.fixed_rows, req.off_lo, lo, hi,
+                                        req.k, req.selected_count, k_pre_new=k_pre_new, write_col=req.write_col,
+                                        return_rows=rows, canonical_order=True)
+        torch.cuda.synchronize()
+        outs.append(got[0] if rows else got)
+    assert torch.equal(outs[0], outs[1])

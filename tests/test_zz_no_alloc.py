@@ -23,7 +23,7 @@ def inputs(gpu, B, h, C, seed, G=8, r=32):
                 k_new=t(B, G, 128), wq_t=idx.wq_t_scaled.contiguous(), wk=idx.wk.contiguous())
 
 
-def step(gpu, x, B, h, C, L, rho, order, noalloc):
+def step(gpu, x, B, h, C, L, rho, order, noalloc, with_rows=True):
     G, r = 8, 32
     req = prepare_request(B, G, C, valid_length=L, query_position=L - 1, rho=rho, device=gpu)
     lo, hi, k, S = req.layout.candidate_lo, req.layout.candidate_hi, req.k, req.selected_count
@@ -36,14 +36,17 @@ def step(gpu, x, B, h, C, L, rho, order, noalloc):
             x["wq_t"].data_ptr(), x["wk"].data_ptr(), x["k_new"].data_ptr(), B, G, h, r, C, lo, hi, L, k, L - 1,
             1.0 / math.sqrt(128), order, P]
     stream = nat.stream_of(gpu)
+    rp, fp = (rows.data_ptr(), flat.data_ptr()) if with_rows else (None, None)
     if noalloc:
-        nat.call("attnlab_sparse_decode_step_noalloc", *head, rows.data_ptr(), flat.data_ptr(), out.data_ptr(), stream)
+        nat.call("attnlab_sparse_decode_step_noalloc", *head, rp, fp, out.data_ptr(), stream)
     else:
         nbytes = nat.lib().attnlab_sparse_decode_workspace(B, G, h, lo, hi, L, k, P)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
         state = torch.zeros(B * G * nat.SELECT_STATE_WORDS, dtype=torch.int32, device=gpu)
-        nat.call("attnlab_sparse_decode_step", *head, state.data_ptr(), ws.data_ptr(), nbytes, rows.data_ptr(),
-                 flat.data_ptr(), out.data_ptr(), stream)
+        nat.call("attnlab_sparse_decode_step", *head, state.data_ptr(), ws.data_ptr(), nbytes, rp, fp, out.data_ptr(),
+                 stream)
+        torch.cuda.synchronize()
+        assert int(state.abs().sum()) == 0, "the step left its select state dirty"
     torch.cuda.synchronize()
     return out, rows, flat, zT
 
@@ -58,6 +61,23 @@ def test_no_alloc_step_matches_the_step(gpu, first, second):
         want = step(gpu, x, B, h, C, L, rho, order, noalloc=False)
         got = step(gpu, x, B, h, C, L, rho, order, noalloc=True)
         for a, b, name in zip(got, want, ("out", "rows", "flat", "zT")):
+            assert torch.equal(a, b), f"call {n + 1}: {name} differs from attnlab_sparse_decode_step"
+
+
+def test_no_alloc_step_without_rows_matches_the_step(gpu):
+    """Without a row list (the step's select-and-attend launch), on the library's own state: two calls in a row, the
+    second smaller, each equal to attnlab_sparse_decode_step bit for bit; a third call with rows afterwards still
+    matches (the fused launch left the library's state zero)."""
+    calls = ((2, 4, 16384 + 64, 16384, 1 / 32, nat.ORDER_POSITION, False),
+             (1, 2, 2048 + 64, 2048, 1 / 16, nat.ORDER_POSITION, False),
+             (1, 2, 2048 + 64, 2048, 1 / 16, nat.ORDER_POSITION, True))
+    for n, (B, h, C, L, rho, order, with_rows) in enumerate(calls):
+        x = inputs(gpu, B, h, C, seed=51 + n)
+        want = step(gpu, x, B, h, C, L, rho, order, noalloc=False, with_rows=with_rows)
+        got = step(gpu, x, B, h, C, L, rho, order, noalloc=True, with_rows=with_rows)
+        names = ("out", "rows", "flat", "zT") if with_rows else ("out", "zT")
+        for a, b, name in zip((got[0], got[1], got[2], got[3]) if with_rows else (got[0], got[3]),
+                              (want[0], want[1], want[2], want[3]) if with_rows else (want[0], want[3]), names):
             assert torch.equal(a, b), f"call {n + 1}: {name} differs from attnlab_sparse_decode_step"
 
 
