@@ -303,9 +303,12 @@ int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int
 
 /*
  * One layer's sparse decode read for one new query: z column write, u projection, candidate scan, top-k, merge with
- * F, gather-free attention. Replaces sparse_decode_step_kernel (decode.py:145-163) with a few launches on `stream`
- * (score prologue and scan; select, tiled in two launches when `state` is given; attend, and the split-K merge
- * when P > 1). Calls sharing a workspace or a select state must be ordered on one stream.
+ * F, gather-free attention. Replaces sparse_decode_step_kernel (decode.py:145-163) with a few launches on `stream`:
+ * the score (u, z column, scan and, with `state`, the key lists of the list select), then the select and the attend.
+ * With neither rows_out nor rows_flat, and the list select applying, those two are one launch: every attend
+ * workgroup selects its row from the key lists and attends its partition (the output bits of the separate launches).
+ * The attend merges split-K partials in-kernel with `state`, else a combine launch does when P > 1. Calls sharing a
+ * workspace or a select state must be ordered on one stream.
  * q_main: [B,G,h,128] bf16 (post-RoPE query); q_cat: [B,G,h*128] bf16 (pre-RoPE query, project_queries order);
  * K/V: [B,G,C,128] bf16; zT: [B,G,r,C] bf16; wq_t: [G,h*128,r]; wk: [G,r,128]; k_new: [B,G,128] (nullable: the
  * z column is not written). F = [0, lo) U [hi, legal); k top candidates; write_col = legal - 1 for the reference's
@@ -314,8 +317,8 @@ int64_t attnlab_sparse_decode_workspace(int B, int G, int h, int lo, int hi, int
  * with neither rows_out nor rows_flat given the row order is not observable (attention is the same over any order of
  * its rows, up to the summation's rounding), and the step runs the position-order select, the faster one.
  * state: select state [B*G, ATTNLAB_SELECT_STATE_WORDS] uint32, zero before the first call; the score kernel fills
- * it and the select kernels clear it, so it stays zero between calls with no memset (the launches stay capturable in
- * a HIP graph). Nullable: the select kernel then runs its own first radix pass on one workgroup per row.
+ * it and the select kernels (in the one-launch form, the row's last workgroup to read it) clear it, so it stays zero
+ * between calls with no memset (the launches stay capturable in a HIP graph). Nullable: the select kernel then runs its own first radix pass on one workgroup per row.
  */
 int attnlab_sparse_decode_step(const uint16_t* q_main, const uint16_t* q_cat, const uint16_t* K, const uint16_t* V,
                                uint16_t* zT, const uint16_t* wq_t, const uint16_t* wk, const uint16_t* k_new,
