@@ -629,6 +629,8 @@ def test_in_kernel_partition_merge_equals_the_combine_kernel(gpu, G, h, P):
     (1, 3, 4, 8192 + 64, 8192, 1 / 8, None, 16),
     (1, 2, 1, 300, 256, 1 / 8, None, None),                  # sinks, picks and recent rows in one partition
     (1, 8, 2, 2048 + 64, 2048, 1 / 32, None, 64),            # S = 132 over 64 partitions: 20 of them empty
+    (1, 8, 6, 2048 + 64, 2048, 1 / 32, None, None),          # three heads per workgroup: the separate launches
+    (2, 4, 3, 4096 + 64, 4096, 1 / 16, None, 4),             # likewise, odd h
 ])
 def test_fused_select_attend_equals_the_separate_stages(gpu, B, G, h, C, L, rho, case, P):
     """A step whose row list does not leave the call selects and attends in one launch (every workgroup of a row
