@@ -69,6 +69,11 @@ int sparse_decode_step_impl(const uint16_t* q_main, const uint16_t* K, const uin
     ATTNLAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, "workspace of %lld bytes needed, got %lld",
                     (long long)L.total, (long long)workspace_bytes);
     ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, "workspace must be 256-byte aligned");
+    // the attend's own checks, here so that the one-launch select and attend cannot refuse the call after the score
+    ATTNLAB_REQUIRE(q_main && K && V && out, "q_main, K, V and out must be device pointers");
+    ATTNLAB_REQUIRE(reinterpret_cast<uintptr_t>(K) % 16 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(q_main) % 16 == 0,
+                    "K, V and q_main must be 16-byte aligned");
     // every check of the select before the first launch: the score kernel adds into the select state, which only the
     // select clears, so a call rejected after the score launch would leave it dirty for the next call
     {

@@ -352,6 +352,16 @@ def test_rejected_call_leaves_the_select_state_clean(gpu):
                  nat.stream_of(gpu))
     torch.cuda.synchronize()
     assert int(state[:B * G * nat.SELECT_STATE_WORDS * 4].abs().sum()) == 0, "the rejected call touched the state"
+    # a K the attend refuses (not 16-byte aligned), in position order with no row list (the one-launch select and
+    # attend): refused before the score launch as well
+    Kmis = torch.empty(K.numel() + 8, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="aligned"):
+        nat.call("attnlab_sparse_decode_step", qm.data_ptr(), qc.data_ptr(), Kmis.data_ptr() + 2, V.data_ptr(),
+                 zT.data_ptr(), idx.wq_t_scaled.data_ptr(), idx.wk.data_ptr(), kn.data_ptr(), B, G, h, 32, C, lo, hi,
+                 L, k, L - 1, 0.088, nat.ORDER_POSITION, 1, state.data_ptr(), ws.data_ptr(), ws.numel(), None, None,
+                 out.data_ptr(), nat.stream_of(gpu))
+    torch.cuda.synchronize()
+    assert int(state[:B * G * nat.SELECT_STATE_WORDS * 4].abs().sum()) == 0, "the rejected call touched the state"
     for canonical in (False, True):
         z = zT.clone()
         _, out2, pos = run_step(gpu, K, V, q, q_pre, k_pre_new, z, idx, L, 1 / 32, canonical)
